@@ -1,0 +1,244 @@
+#!/usr/bin/env python3
+"""Benchmark: µs per INT4 FFN decode call (M=1) on one MI355X, plus achieved HBM GB/s.
+
+Workload (default): the Qwen3-4B-shaped dense FFN, hidden 2560,
+intermediate 9728, INT4 group-128 weights with BF16 scales, BF16 activation, one decode token.
+Weights are synthetic (BF16 ~N(0, 0.02), quantized on the device by the library's quantizer,
+re-laid into tile order), activations BF16 ~N(0, 1). 16 distinct weight sets (616 MB) rotate
+so the 256 MB Infinity Cache cannot serve the stream; one "step" is one FFN call (fused
+gate/up/SiLU kernel + down kernel) on the next set, inputs already resident in HBM.
+
+``--config 2`` runs the 27B FFN (hidden 5120, intermediate 17408) over 64 distinct layers
+(8.8 GB); ``--config 4`` its tp=2 rank-0 slice; ``--config 0`` the single K=2560, N=9728
+linear; ``--config 3`` config 1 at M = --m.
+
+Prints ONE JSON line. ``roofline`` is the dominant kernel's (the fused gate/up/SiLU GEMV):
+algorithmic bytes per launch (packed nibbles + BF16 scales of its weight) over its average
+duration, from HIP events recorded on the launch stream around each launch in a second timed
+pass. ``cpu_baseline`` times the CPU dequant+matmul path (numpy, BLAS) on rank 0 over a
+bounded sample.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "haskell-infer-demo_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+CACHE_ROTATE_BYTES = 512 << 20   # rotate at least this many weight bytes (MALL is 256 MB)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3, 4))
+    ap.add_argument("--m", type=int, default=4, help="rows for --config 3")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    return ap.parse_args()
+
+
+def shapes(cfg, m):
+    """(hidden, intermediate, M, layers-or-sets, name)."""
+    if cfg == 0:
+        return 2560, 9728, 1, "config0: single W4A16 linear M=1 K=2560 N=9728"
+    if cfg == 1:
+        return 2560, 9728, 1, "config1: Qwen3-4B dense FFN decode M=1 H=2560 I=9728"
+    if cfg == 2:
+        return 5120, 17408, 1, "config2: 27B dense FFN decode M=1 H=5120 I=17408, 64 layers"
+    if cfg == 3:
+        return 2560, 9728, m, f"config3: Qwen3-4B dense FFN verify rows M={m}"
+    return 5120, 8704, 1, "config4: tp=2 rank-0 slice of config2 (I/2=8704), FP32 partial"
+
+
+def make_sets(torch, w4a16, hidden, inter, count, linear_only, seed=1234):
+    """Device-generated weight sets in tile order (gate/up pair + down), or single linears."""
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    sets = []
+    for _ in range(count):
+        def quantized(n, k):
+            w = (torch.randn(n, k, generator=gen, device=dev) * 0.02).to(torch.bfloat16).float()
+            p, s = w4a16.quantize_device(w)
+            del w
+            return p, s
+
+        if linear_only:
+            p, s = quantized(inter, hidden)
+            sets.append((w4a16.TiledWeight.from_device_artifact(p, s, inter, hidden), None, (p, s)))
+            continue
+        gp, gs = quantized(2 * inter, hidden)   # gate rows then up rows, as the F1 pair
+        dp, ds = quantized(hidden, inter)
+        gu = w4a16.TiledWeight.from_device_artifact(gp, gs, 2 * inter, hidden, pair=True)
+        dn = w4a16.TiledWeight.from_device_artifact(dp, ds, hidden, inter)
+        keep = (gp, gs, dp, ds) if not sets else None   # artifact of set 0 for the CPU leg
+        sets.append((gu, dn, keep))
+    torch.cuda.synchronize()
+    return sets
+
+
+def cpu_baseline(sets, hidden, inter, m, linear_only, seconds):
+    import numpy as np
+
+    from oracle import oracle
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        cores = os.cpu_count() or 1
+    keep = sets[0][2]
+    x = oracle.synth_activation(m, hidden, 7)
+    if linear_only:
+        p, s = (t.cpu().numpy() for t in keep)
+        s = s.view(np.uint16)
+
+        def run():
+            w = oracle.dequantize_numpy(p, s, inter, hidden)
+            return oracle.bf16_bits(oracle.bf16_to_f32(x).reshape(m, hidden) @ w.T)
+    else:
+        gp, gs, dp, ds = (t.cpu().numpy() for t in keep)
+        gs, ds = gs.view(np.uint16), ds.view(np.uint16)
+
+        def run():
+            return oracle.ffn_cpu_baseline(x, gp, gs, dp, ds, hidden, inter)
+    run()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        run()
+        times.append((time.perf_counter() - t0) * 1e6)
+        if len(times) >= 50:
+            break
+    times.sort()
+    return {"value": round(times[len(times) // 2], 1), "unit": "us per call", "cores": cores,
+            "kind": "port",
+            "sample": f"{len(times)} calls of numpy dequantize-per-call + FP32 BLAS matmul "
+                      f"(BF16 rounding at the reference's points) on one weight set, median"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(the tensor-parallel slice is benchmarked on one GPU as --config 4)",
+              file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import w4a16
+
+    hidden, inter, m, name = shapes(args.config, args.m)
+    linear_only = args.config == 0
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    if linear_only:
+        per_set = inter * hidden // 2 + inter * hidden // 128 * 2
+    else:
+        per_set = 3 * (inter * hidden // 2 + inter * hidden // 128 * 2)
+    count = 64 if args.config == 2 else max(16, -(-CACHE_ROTATE_BYTES // per_set))
+    print(f"bench: {name}; generating {count} weight sets ({count * per_set / 2**20:.0f} MiB)",
+          file=sys.stderr, flush=True)
+    sets = make_sets(torch, w4a16, hidden, inter, count, linear_only)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    x = torch.randn(m, hidden, generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
+    act = torch.empty(m, inter, dtype=torch.int16, device=dev)
+    partial = args.config == 4
+    out = torch.empty(m, inter if linear_only else hidden,
+                      dtype=torch.float32 if partial else torch.int16, device=dev)
+    stream = torch.cuda.current_stream()
+    s_handle = stream.cuda_stream
+
+    def step(i):
+        gu, dn, _ = sets[i % count]
+        if linear_only:
+            w4a16.gemm_int4_bf16(x, gu, out, stream=s_handle)
+        else:
+            w4a16.mlp_int4(x, gu, dn, out=out, act_ws=act, partial_f32=partial, stream=s_handle)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(args.steps):
+        step(i)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_total = start.elapsed_time(stop)
+    us_per_call = ms_total * 1e3 / args.steps
+
+    # Second pass: events around each launch of the dominant kernel (and of the down kernel).
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    down_out = torch.empty(m, hidden, dtype=torch.int16, device=dev)
+    for i in range(args.steps):
+        gu, dn, _ = sets[i % count]
+        e = evs[i]
+        e[0].record(stream)
+        if linear_only:
+            w4a16.gemm_int4_bf16(x, gu, out, stream=s_handle)
+            e[1].record(stream)
+        else:
+            w4a16.gate_up_silu(x, gu, act, stream=s_handle)
+            e[1].record(stream)
+            w4a16.gemm_int4_bf16(act, dn, down_out, stream=s_handle)
+        e[2].record(stream)
+    torch.cuda.synchronize()
+    k1 = sorted(e[0].elapsed_time(e[1]) * 1e3 for e in evs)
+    k2 = sorted(e[1].elapsed_time(e[2]) * 1e3 for e in evs)
+    k1_avg = sum(k1) / len(k1)
+    k2_avg = sum(k2) / len(k2)
+    if linear_only:
+        dom_bytes = per_set
+        dom_name = "gemv_tiles_kernel<false,false> (gemm_int4_bf16)"
+    else:
+        dom_bytes = 2 * inter * hidden // 2 + 2 * inter * hidden // 128 * 2
+        dom_name = "gemv_tiles_kernel<true,false> (fused gate/up + SiLU x up)"
+    achieved = dom_bytes / (k1_avg * 1e-6) / 1e9
+    ffn_gbs = per_set / (us_per_call * 1e-6) / 1e9
+
+    result = {
+        "metric": "µs per INT4 FFN decode call (M=1) + achieved HBM GB/s vs peak, 1 MI355X",
+        "value": round(us_per_call, 3),
+        "unit": "us per FFN call" if not linear_only else "us per linear call",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_total / args.steps, 6),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int4 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic (device-generated BF16 ~N(0,0.02) weights quantized by the library, "
+                "BF16 ~N(0,1) activations)",
+        "config": {"workload": name, "hidden": hidden, "intermediate": inter, "M": m,
+                   "weight_sets_rotated": count, "bytes_per_call": per_set,
+                   "ffn_achieved_GBps": round(ffn_gbs, 1),
+                   "ffn_frac_of_peak": round(ffn_gbs / HBM_PEAK_GBS, 4),
+                   "wall_us_per_call": round(wall * 1e6 / args.steps, 3),
+                   "kernel_avg_us": {"dominant": round(k1_avg, 3), "second": round(k2_avg, 3)}},
+        "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": dom_bytes},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(sets, hidden, inter, m, linear_only,
+                                              args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

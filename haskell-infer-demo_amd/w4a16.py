@@ -1,0 +1,291 @@
+"""Host-side binding of libw4a16.so, the MI355X W4A16 dense-FFN decode library.
+
+This module mirrors the reference's operator interface for the path:
+
+* ``gemm_int4_bf16(a, packed, scales, out, M, N, K, group, stream)`` - reference
+  csrc/include/layers.h:376-377 (C++, throws) -> here a status-returning C entry point; the Python
+  wrapper raises ``W4A16Error`` where the reference throws ``std::invalid_argument``.
+* ``kernel_silu_mul_packed(out, packed, tokens, intermediate)`` - reference
+  csrc/kernels/silu.cu:78-95.
+* ``mlp_int4`` - the INT4 branch of ``mlp_from_normed`` (reference csrc/kernels/layers.cu:126-145).
+* ``test_gemm_int4`` - the reference bridge symbol (tests/kernels/kernel_bridge.cu:83-95).
+
+Device tensors are torch CUDA tensors (on ROCm, HIP memory); torch is used only for device memory
+and streams. There is no CPU fallback: if the library is missing the import fails.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libw4a16.so")
+
+GROUP = 128
+TILE_ROWS = 8
+
+W4A16_OK = 0
+W4A16_ERR_HIP = -1
+W4A16_ERR_ALLOC = -2
+W4A16_ERR_WEIGHTS = -3
+W4A16_ERR_CONFIG = -4
+W4A16_ERR_STATE = -5
+
+
+class W4A16Error(RuntimeError):
+    """A nonzero status from the library, with its thread-local reason."""
+
+    def __init__(self, status, message):
+        super().__init__(f"{message} (status {status})")
+        self.status = status
+
+
+_vp = ctypes.c_void_p
+_ll = ctypes.c_longlong
+_i = ctypes.c_int
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "w4a16_last_error": (ctypes.c_char_p, []),
+    "w4a16_layout_init": (_i, [_ll, _ll, _ll, ctypes.POINTER(_ll), ctypes.POINTER(_ll)]),
+    "w4a16_f32_to_bf16": (ctypes.c_uint16, [ctypes.c_float]),
+    "w4a16_bf16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+    "w4a16_quantize_int4": (_i, [_ll, _ll, _vp, _vp, _vp]),
+    "w4a16_dequantize_int4": (_i, [_ll, _ll, _vp, _vp, _vp]),
+    "w4a16_tile_pack_host": (_i, [_ll, _ll, _i, _vp, _vp, _vp, _vp]),
+    "w4a16_tile_unpack_host": (_i, [_ll, _ll, _i, _vp, _vp, _vp, _vp]),
+    "w4a16_tile_pack_device": (_i, [_ll, _ll, _i, _vp, _vp, _vp, _vp, _vp]),
+    "w4a16_dequant_tiled_device": (_i, [_ll, _ll, _i, _vp, _vp, _vp, _vp]),
+    "w4a16_quantize_device": (_i, [_ll, _ll, _vp, _vp, _vp, _vp, _vp]),
+    "gemm_int4_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "silu_mul_packed_bf16": (_i, [_vp, _vp, _i, _i, _vp]),
+    "gate_up_silu_int4_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "mlp_int4_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "mlp_int4_partial_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "test_gemm_int4": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i]),
+    "test_silu_mul_packed": (_i, [_vp, _vp, _i, _i]),
+}
+
+
+def header_symbols():
+    """Function names declared in include/w4a16.h (the exported C ABI)."""
+    import re
+
+    path = os.path.join(_HERE, "..", "include", "w4a16.h")
+    with open(path) as handle:
+        text = handle.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b([a-z_0-9]+)\s*\(", text)) - {"defined"})
+
+
+def load_library(path=LIB_PATH):
+    if not os.path.exists(path):
+        raise ImportError(f"libw4a16.so is not built ({path}); run __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return lib
+
+
+lib = load_library()
+
+
+def last_error():
+    return lib.w4a16_last_error().decode(errors="replace")
+
+
+def _check(status, what):
+    if status != W4A16_OK:
+        raise W4A16Error(status, f"{what}: {last_error()}")
+
+
+def _ptr(t):
+    """Address of a torch tensor or numpy array (None -> NULL)."""
+    if t is None:
+        return None
+    if isinstance(t, np.ndarray):
+        return t.ctypes.data
+    return t.data_ptr()
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+# ----------------------------------------------------------------------------------------------
+# Format (host)
+# ----------------------------------------------------------------------------------------------
+
+
+def layout_init(n, k, group=GROUP):
+    pb, sc = _ll(0), _ll(0)
+    _check(lib.w4a16_layout_init(n, k, group, ctypes.byref(pb), ctypes.byref(sc)), "layout_init")
+    return pb.value, sc.value
+
+
+def quantize_int4(weights):
+    """FP32 [N, K] -> (packed u8 [N, K/2], scales u16 [N, K/128]), the converter's arithmetic."""
+    w = np.ascontiguousarray(weights, dtype=np.float32)
+    n, k = w.shape
+    pb, sc = layout_init(n, k)
+    packed = np.empty((n, k // 2), dtype=np.uint8)
+    scales = np.empty((n, k // GROUP), dtype=np.uint16)
+    _check(lib.w4a16_quantize_int4(n, k, _ptr(w), _ptr(packed), _ptr(scales)), "quantize_int4")
+    return packed, scales
+
+
+def dequantize_int4(packed, scales, n, k):
+    out = np.empty((n, k), dtype=np.float32)
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    s = np.ascontiguousarray(scales, dtype=np.uint16)
+    _check(lib.w4a16_dequantize_int4(n, k, _ptr(p), _ptr(s), _ptr(out)), "dequantize_int4")
+    return out
+
+
+def tile_pack_host(packed, scales, n, k, pair=False):
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    s = np.ascontiguousarray(scales, dtype=np.uint16)
+    pt = np.empty(n * k // 2, dtype=np.uint8)
+    st = np.empty(n * (k // GROUP), dtype=np.uint16)
+    _check(lib.w4a16_tile_pack_host(n, k, int(pair), _ptr(p), _ptr(s), _ptr(pt), _ptr(st)),
+           "tile_pack_host")
+    return pt, st
+
+
+def tile_unpack_host(packed_tiled, scales_tiled, n, k, pair=False):
+    pt = np.ascontiguousarray(packed_tiled, dtype=np.uint8)
+    st = np.ascontiguousarray(scales_tiled, dtype=np.uint16)
+    p = np.empty((n, k // 2), dtype=np.uint8)
+    s = np.empty((n, k // GROUP), dtype=np.uint16)
+    _check(lib.w4a16_tile_unpack_host(n, k, int(pair), _ptr(pt), _ptr(st), _ptr(p), _ptr(s)),
+           "tile_unpack_host")
+    return p, s
+
+
+# ----------------------------------------------------------------------------------------------
+# Device operands
+# ----------------------------------------------------------------------------------------------
+
+
+class TiledWeight:
+    """An INT4 weight resident on the device in tile order (packed u8 + BF16 scale bits)."""
+
+    def __init__(self, packed, scales, n, k, pair):
+        self.packed, self.scales, self.n, self.k, self.pair = packed, scales, n, k, pair
+
+    @property
+    def nbytes(self):
+        return self.packed.numel() + self.scales.numel() * 2
+
+    @classmethod
+    def from_artifact(cls, packed, scales, n, k, pair=False, device="cuda", stream=None):
+        """Upload artifact-layout (row-major) packed/scales and re-lay them on the device."""
+        import torch
+
+        p = torch.as_tensor(np.ascontiguousarray(packed, dtype=np.uint8)).reshape(-1).to(device)
+        s = torch.as_tensor(np.ascontiguousarray(scales, dtype=np.uint16).view(np.int16))
+        s = s.reshape(-1).to(device)
+        return cls.from_device_artifact(p, s, n, k, pair, stream)
+
+    @classmethod
+    def from_device_artifact(cls, p, s, n, k, pair=False, stream=None):
+        import torch
+
+        pt = torch.empty_like(p)
+        st = torch.empty_like(s)
+        _check(lib.w4a16_tile_pack_device(n, k, int(pair), p.data_ptr(), s.data_ptr(),
+                                          pt.data_ptr(), st.data_ptr(), _stream(stream)),
+               "tile_pack_device")
+        return cls(pt, st, n, k, pair)
+
+    def dequantize(self, stream=None):
+        import torch
+
+        out = torch.empty((self.n, self.k), dtype=torch.float32, device=self.packed.device)
+        _check(lib.w4a16_dequant_tiled_device(self.n, self.k, int(self.pair),
+                                              self.packed.data_ptr(), self.scales.data_ptr(),
+                                              out.data_ptr(), _stream(stream)),
+               "dequant_tiled_device")
+        return out
+
+
+def quantize_device(weights, stream=None):
+    """FP32 [N, K] CUDA tensor -> artifact-layout (packed, scales) CUDA tensors."""
+    import torch
+
+    n, k = weights.shape
+    layout_init(n, k)
+    packed = torch.empty(n * k // 2, dtype=torch.uint8, device=weights.device)
+    scales = torch.empty(n * (k // GROUP), dtype=torch.int16, device=weights.device)
+    status = torch.zeros(1, dtype=torch.int32, device=weights.device)
+    _check(lib.w4a16_quantize_device(n, k, weights.contiguous().data_ptr(), packed.data_ptr(),
+                                     scales.data_ptr(), status.data_ptr(), _stream(stream)),
+           "quantize_device")
+    if int(status.item()) != 0:
+        raise W4A16Error(W4A16_ERR_CONFIG, "quantize_device: a nonfinite input or a scale the "
+                                           "format cannot hold")
+    return packed, scales
+
+
+# ----------------------------------------------------------------------------------------------
+# Compute
+# ----------------------------------------------------------------------------------------------
+
+
+def gemm_int4_bf16(a, w, out=None, stream=None):
+    """out[M, N] = a[M, K] @ W^T; a/out are int16-viewed BF16 (or torch.bfloat16) tensors."""
+    import torch
+
+    m = a.shape[0]
+    if out is None:
+        out = torch.empty((m, w.n), dtype=a.dtype, device=a.device)
+    _check(lib.gemm_int4_bf16(a.data_ptr(), w.packed.data_ptr(), w.scales.data_ptr(),
+                              out.data_ptr(), m, w.n, w.k, GROUP, _stream(stream)),
+           "gemm_int4_bf16")
+    return out
+
+
+def kernel_silu_mul_packed(out, packed, tokens, intermediate, stream=None):
+    _check(lib.silu_mul_packed_bf16(out.data_ptr(), packed.data_ptr(), tokens, intermediate,
+                                    _stream(stream)), "silu_mul_packed")
+    return out
+
+
+def gate_up_silu(x, gu, act=None, stream=None):
+    import torch
+
+    m, h = x.shape
+    inter = gu.n // 2
+    if act is None:
+        act = torch.empty((m, inter), dtype=x.dtype, device=x.device)
+    _check(lib.gate_up_silu_int4_bf16(x.data_ptr(), gu.packed.data_ptr(), gu.scales.data_ptr(),
+                                      act.data_ptr(), m, h, inter, _stream(stream)),
+           "gate_up_silu")
+    return act
+
+
+def mlp_int4(x, gu, dn, out=None, act_ws=None, partial_f32=False, stream=None):
+    """The INT4 dense MLP on already-normalised activations x [M, H] (BF16 bits)."""
+    import torch
+
+    m, h = x.shape
+    inter = gu.n // 2
+    if act_ws is None:
+        act_ws = torch.empty((m, inter), dtype=x.dtype, device=x.device)
+    if out is None:
+        out = torch.empty((m, h), dtype=torch.float32 if partial_f32 else x.dtype,
+                          device=x.device)
+    fn = lib.mlp_int4_partial_f32 if partial_f32 else lib.mlp_int4_bf16
+    _check(fn(x.data_ptr(), gu.packed.data_ptr(), gu.scales.data_ptr(), dn.packed.data_ptr(),
+              dn.scales.data_ptr(), out.data_ptr(), act_ws.data_ptr(), m, h, inter,
+              _stream(stream)), "mlp_int4")
+    return out

@@ -1,0 +1,153 @@
+/*
+ * w4a16.h - C ABI of the MI355X (gfx950) weight-only INT4 dense-FFN decode path.
+ *
+ * The artifact format is the reference's frozen INT4 format (reference
+ * csrc/include/linear_weight.h:5-13): symmetric signed INT4 codes in 128-wide K groups, BF16
+ * scales, two two's-complement nibbles per byte with the lower K index in the low nibble,
+ * row-major packed [N, K/2] plus row-major scales [N, K/128]. Nothing here changes it.
+ *
+ * On the device the library keeps a re-laid copy ("tile order") of every weight: a pure
+ * permutation of the nibbles and of the scales, chosen so one wave64 load instruction moves
+ * 1 KiB of one 8-row tile and so the fused gate/up kernel sees gate row i and up row i in the
+ * same tile. Compute entry points take device pointers in tile order; w4a16_tile_pack_* produce
+ * it from the artifact layout, and w4a16_tile_unpack_host is the exact inverse.
+ *
+ * Conventions (all entry points):
+ *   - BF16 tensors are passed as uint16_t bit patterns, FP32 as float.
+ *   - Every function returns W4A16_OK (0) or a negative W4A16_ERR_* status and never throws;
+ *     the reason is in the calling thread's w4a16_last_error().
+ *   - `stream` is a hipStream_t (NULL = the default stream). Device entry points are
+ *     asynchronous on it and perform no host synchronisation.
+ *   - Device pointers must come from hipMalloc (or a torch CUDA tensor) on the current device.
+ */
+#ifndef W4A16_H
+#define W4A16_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes mirror the engine's ENGINE_* codes (reference csrc/include/engine.h:264-270). */
+#define W4A16_OK 0
+#define W4A16_ERR_HIP (-1)     /* HIP runtime error (reference ENGINE_ERR_CUDA) */
+#define W4A16_ERR_ALLOC (-2)   /* device allocation failed */
+#define W4A16_ERR_WEIGHTS (-3) /* artifact missing, malformed, hash or shape mismatch */
+#define W4A16_ERR_CONFIG (-4)  /* invalid argument or unsupported shape */
+#define W4A16_ERR_STATE (-5)   /* invalid handle state */
+
+#define W4A16_GROUP 128
+#define W4A16_TILE_ROWS 8
+
+/* Thread-local reason for the last failure on this thread ("" if none).
+ * Replaces linear_last_error / quant_manifest_last_error / engine_last_error
+ * (reference csrc/linear_weight.cpp:16-28, csrc/quant_manifest.c:29-41). */
+const char *w4a16_last_error(void);
+
+/* ---------------------------------------------------------------------------------------
+ * Format (host, CPU only). Same rules as the reference's linear_weight.h.
+ * ------------------------------------------------------------------------------------- */
+
+/* Extents of an [n, k] weight: refuses n,k <= 0, group != 128, k % 128, n % 8.
+ * Replaces linear_layout_init (reference csrc/linear_weight.cpp:57-86). */
+int w4a16_layout_init(long long n, long long k, long long group, long long *packed_bytes,
+                      long long *scale_count);
+
+/* BF16 round-to-nearest-even (reference csrc/linear_weight.cpp:34-51). */
+uint16_t w4a16_f32_to_bf16(float value);
+float w4a16_bf16_to_f32(uint16_t bits);
+
+/* The converter's quantizer: FP32 [n, k] row-major -> artifact payload + BF16 scales.
+ * Replaces linear_quantize_int4 (reference csrc/linear_weight.cpp:108-176). */
+int w4a16_quantize_int4(long long n, long long k, const float *weights, uint8_t *packed,
+                        uint16_t *scales);
+
+/* The format's dequantizer (refuses nibble 0x8 and bad scales).
+ * Replaces linear_dequantize_int4 (reference csrc/linear_weight.cpp:178-216). */
+int w4a16_dequantize_int4(long long n, long long k, const uint8_t *packed,
+                          const uint16_t *scales, float *out);
+
+/* ---------------------------------------------------------------------------------------
+ * Tile order (new; the reference uploads row-major: csrc/engine.cu:2370-2395).
+ *
+ * `pair` = 0: an ordinary [n, k] weight. `pair` = 1: the F1 gate/up pair [n = 2I, k] whose
+ * rows 0..I-1 are gate and I..2I-1 are up (reference scripts/quantize_weights.py:236-276);
+ * tile t then holds gate rows 4t..4t+3 and up rows 4t..4t+3 (needs I % 4 == 0).
+ * Both buffers keep their artifact sizes (n*k/2 bytes and n*k/128 scales).
+ * ------------------------------------------------------------------------------------- */
+int w4a16_tile_pack_host(long long n, long long k, int pair, const uint8_t *packed,
+                         const uint16_t *scales, uint8_t *packed_tiled, uint16_t *scales_tiled);
+int w4a16_tile_unpack_host(long long n, long long k, int pair, const uint8_t *packed_tiled,
+                           const uint16_t *scales_tiled, uint8_t *packed, uint16_t *scales);
+/* The same permutation on the device (artifact layout already uploaded). */
+int w4a16_tile_pack_device(long long n, long long k, int pair, const uint8_t *packed,
+                           const uint16_t *scales, uint8_t *packed_tiled,
+                           uint16_t *scales_tiled, void *stream);
+/* Dequantize a tile-order weight to FP32 row-major [n, k] on the device: the check that the
+ * re-laid operand is bit-exact with the format's dequantizer. */
+int w4a16_dequant_tiled_device(long long n, long long k, int pair, const uint8_t *packed_tiled,
+                               const uint16_t *scales_tiled, float *out, void *stream);
+/* Quantize FP32 [n, k] on the device, bit-exact with w4a16_quantize_int4 (used to produce
+ * large synthetic weight sets quickly). Writes the artifact (row-major) layout. Inputs must be
+ * finite and every group's rounded scale positive; violations are reported through
+ * `status_dev` (one int32 on the device, left 0 on success). */
+int w4a16_quantize_device(long long n, long long k, const float *weights, uint8_t *packed,
+                          uint16_t *scales, int *status_dev, void *stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Compute (device pointers, tile order).
+ * ------------------------------------------------------------------------------------- */
+
+/* out[M, N] (BF16) = a[M, K] (BF16) x W^T, FP32 accumulation, W in tile order (pair = 0).
+ * Same refusals as the reference wrapper: M,N < 0, K <= 0 or group <= 0; M == 0 or N == 0 is a
+ * no-op; null buffers; K % group; group % 8. Replaces gemm_int4_bf16 (reference
+ * csrc/include/layers.h:376-377, csrc/kernels/gemm_quant.cu:204-254), which throws instead. */
+int gemm_int4_bf16(const uint16_t *a, const uint8_t *packed, const uint16_t *scales,
+                   uint16_t *out, int M, int N, int K, int group, void *stream);
+
+/* act[t, i] = BF16(silu(g) * u) over the row-interleaved [tokens, 2I] buffer.
+ * Replaces kernel_silu_mul_packed (reference csrc/kernels/silu.cu:78-95). */
+int silu_mul_packed_bf16(uint16_t *out, const uint16_t *packed, int tokens, int intermediate,
+                         void *stream);
+
+/* act[M, I] (BF16) = BF16(silu(BF16(x W_gate^T)) * BF16(x W_up^T)) from the gate/up pair in
+ * tile order (pair = 1), one kernel: the [M, 2I] gate/up output never reaches memory. */
+int gate_up_silu_int4_bf16(const uint16_t *x, const uint8_t *gu_packed,
+                           const uint16_t *gu_scales, uint16_t *act, int M, int hidden,
+                           int intermediate, void *stream);
+
+/* The INT4 branch of the dense MLP (reference csrc/kernels/layers.cu:126-145): fused
+ * gate/up/SiLU, then down. `act_ws` is caller workspace of M * intermediate BF16.
+ * out [M, hidden] BF16. */
+int mlp_int4_bf16(const uint16_t *normed, const uint8_t *gu_packed, const uint16_t *gu_scales,
+                  const uint8_t *dn_packed, const uint16_t *dn_scales, uint16_t *out,
+                  uint16_t *act_ws, int M, int hidden, int intermediate, void *stream);
+
+/* Tensor-parallel slice: as mlp_int4_bf16, but the down projection's FP32 partial is written
+ * unrounded (out_f32 [M, hidden]), to be summed across ranks before rounding. */
+int mlp_int4_partial_f32(const uint16_t *normed, const uint8_t *gu_packed,
+                         const uint16_t *gu_scales, const uint8_t *dn_packed,
+                         const uint16_t *dn_scales, float *out_f32, uint16_t *act_ws, int M,
+                         int hidden, int intermediate, void *stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Test bridges (host pointers, artifact layout; synchronous).
+ * ------------------------------------------------------------------------------------- */
+
+/* Same symbol and argument meaning as the reference bridge
+ * (reference tests/kernels/kernel_bridge.cu:83-95): host buffers in the artifact layout; the
+ * library uploads, re-lays, runs gemm_int4_bf16 and downloads. Returns 0, or nonzero on a
+ * refusal or error. */
+int test_gemm_int4(void *out, const void *a, const void *packed, const void *scales, int M,
+                   int N, int K, int group);
+
+/* Same as the reference bridge's test_silu_mul_packed (kernel_bridge.cu:66-78). */
+int test_silu_mul_packed(void *out, const void *packed, int tokens, int intermediate);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A16_H */

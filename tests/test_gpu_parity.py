@@ -1,0 +1,226 @@
+"""Parity of the HIP path with the CPU oracle, on cuda:0 (marked ``gpu``).
+
+Bars: dequantized tiles bit-exact with the format's dequantizer; FFN and
+GEMV outputs within rel-L2 <= 1e-3 and <= 2 BF16 ULP (ULP taken at max(|ref|, rms(ref)/64), see
+conftest.parity_metrics) of the oracle's double-accumulated dequant-then-matmul with the
+reference's BF16 rounding points. The reference's own kernel gate
+(tests/test_quantization_kernel.py:130-136: max_rel <= 8e-3, rms_rel <= 4e-3 of max|ref|) is run
+on its own shapes through the same-named bridge symbol test_gemm_int4.
+"""
+
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import w4a16
+from conftest import assert_parity, bf16_f32
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def to_dev(arr, cuda):
+    import torch
+
+    a = np.ascontiguousarray(arr)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).to(cuda)
+
+
+def from_dev(t):
+    a = t.cpu().numpy()
+    return a.view(np.uint16) if a.dtype == np.int16 else a
+
+
+def make_weight(n, k, seed):
+    w = oracle.synth_weight(n, k, seed)
+    return oracle.quantize(w)
+
+
+def make_ffn(hidden, inter, layer=0):
+    """Gate/up pair [2I, H] (gate rows then up rows) and down [H, I], seeds 1000+3*layer+role."""
+    gp, gs = make_weight(inter, hidden, 1000 + 3 * layer)
+    up, us = make_weight(inter, hidden, 1001 + 3 * layer)
+    dp, ds = make_weight(hidden, inter, 1002 + 3 * layer)
+    return np.concatenate([gp, up]), np.concatenate([gs, us]), dp, ds
+
+
+# ---- the tile order on the device ---------------------------------------------------------------
+
+def test_tiled_dequant_bit_exact(cuda):
+    vec = np.load(os.path.join(GOLDEN, "quantize_vectors.npz"), allow_pickle=False)
+    for name in vec["case_names"]:
+        name = str(name)
+        p, s = vec[f"{name}_packed"], vec[f"{name}_scales"]
+        n, k = p.shape[0], p.shape[1] * 2
+        for pair in (False, True):
+            say(f"tiled dequant {name} n={n} k={k} pair={pair}")
+            w = w4a16.TiledWeight.from_artifact(p, s, n, k, pair=pair, device=cuda)
+            hp, hs = w4a16.tile_pack_host(p, s, n, k, pair)
+            assert np.array_equal(from_dev(w.packed), hp)
+            assert np.array_equal(from_dev(w.scales), hs)
+            deq = from_dev(w.dequantize()).view(np.uint32)
+            want = oracle.dequantize_numpy(p, s, n, k).view(np.uint32)
+            assert np.array_equal(deq, want), name
+            if f"{name}_dequant_f32bits" in vec:
+                assert np.array_equal(deq, vec[f"{name}_dequant_f32bits"].reshape(n, k))
+
+
+def test_quantize_device_bit_exact(cuda):
+    import torch
+
+    gen = torch.Generator(device=cuda)
+    gen.manual_seed(5)
+    for n, k, std in ((64, 2560, 0.02), (256, 512, 1.0), (8, 128, 1e-3)):
+        say(f"quantize_device n={n} k={k}")
+        w = (torch.randn(n, k, generator=gen, device=cuda) * std).to(torch.bfloat16).float()
+        w[0, :128] = 0.0
+        w[1, :8] = torch.tensor([0.0, 1.0, -1.0, -7.0, 7.0, 3.0, -3.0, 2.0], device=cuda)
+        p, s = w4a16.quantize_device(w)
+        hp, hs = oracle.quantize(w.cpu().numpy())
+        assert np.array_equal(from_dev(p).reshape(n, -1), hp)
+        assert np.array_equal(from_dev(s).reshape(n, -1), hs)
+    bad = torch.zeros(8, 128, device=cuda)
+    bad[0, 0] = float("nan")
+    with pytest.raises(w4a16.W4A16Error):
+        w4a16.quantize_device(bad)
+
+
+# ---- GEMV (gemm_int4_bf16, M = 1) ----------------------------------------------------------------
+
+@pytest.mark.parametrize("n,k", [(9728, 2560), (2560, 9728), (5120, 17408), (8704, 5120),
+                                 (256, 128), (1024, 384), (24, 1152)])
+def test_gemv_parity(cuda, n, k):
+    say(f"gemv n={n} k={k}")
+    p, s = make_weight(n, k, seed=n + k)
+    x = oracle.synth_activation(1, k, seed=7)
+    w = w4a16.TiledWeight.from_artifact(p, s, n, k, device=cuda)
+    out = from_dev(w4a16.gemm_int4_bf16(to_dev(x, cuda), w))
+    ref = oracle.gemm_bf16(x, p, s, n, k)
+    assert_parity(out, ref, f"gemv {n}x{k}")
+
+
+def test_gemv_closed_forms(cuda):
+    n, k = 512, 2560
+    p, s = make_weight(n, k, seed=3)
+    w = w4a16.TiledWeight.from_artifact(p, s, n, k, device=cuda)
+    deq = oracle.dequantize_numpy(p, s, n, k)
+    say("gemv zero activation")
+    z = from_dev(w4a16.gemm_int4_bf16(to_dev(np.zeros((1, k), np.uint16), cuda), w))
+    assert not bf16_f32(z).any()
+    for col in (0, 1, 127, 128, 1001, k - 1):
+        say(f"gemv one-hot column {col}")
+        x = np.zeros((1, k), np.uint16)
+        x[0, col] = 0x3F80
+        got = from_dev(w4a16.gemm_int4_bf16(to_dev(x, cuda), w))[0]
+        assert np.array_equal(got, oracle.bf16_bits(deq[:, col])), col
+
+
+# ---- SiLU x mul, fused gate/up, whole FFN --------------------------------------------------------
+
+def test_silu_mul_packed(cuda):
+    rng = np.random.default_rng(4)
+    tokens, inter = 3, 4096
+    g = rng.normal(0, 4, size=(tokens, inter)).astype(np.float32)
+    g[0, :6] = [0.0, -0.0, 88.0, -88.0, 1e-20, -120.0]
+    u = rng.normal(0, 1, size=(tokens, inter)).astype(np.float32)
+    packed = np.concatenate([oracle.bf16_bits(g), oracle.bf16_bits(u)], axis=1)
+    want = oracle.silu_mul_packed(packed, tokens, inter)
+    say("silu_mul_packed kernel")
+    import torch
+
+    out = torch.empty((tokens, inter), dtype=torch.int16, device=cuda)
+    w4a16.kernel_silu_mul_packed(out, to_dev(packed, cuda), tokens, inter)
+    got = from_dev(out)
+    m = assert_parity(got, want, "silu_mul_packed", rel_l2=1e-5, max_ulp=1.0)
+    assert m["n_over_1ulp"] == 0
+    # via the reference-shaped host bridge
+    host = np.zeros((tokens, inter), np.uint16)
+    assert w4a16.lib.test_silu_mul_packed(host.ctypes.data, packed.ctypes.data, tokens, inter) == 0
+    assert np.array_equal(host, got)
+
+
+def test_gate_up_silu_parity(cuda):
+    hidden, inter = 2560, 9728
+    say("gate_up_silu C1")
+    gup, gus, _, _ = make_ffn(hidden, inter)
+    x = oracle.synth_activation(1, hidden, seed=7)
+    gu = w4a16.TiledWeight.from_artifact(gup, gus, 2 * inter, hidden, pair=True, device=cuda)
+    act = from_dev(w4a16.gate_up_silu(to_dev(x, cuda), gu))
+    mid = oracle.gemm_bf16(x, gup, gus, 2 * inter, hidden)
+    want = oracle.silu_mul_packed(mid, 1, inter)
+    assert_parity(act, want, "gate_up_silu C1")
+
+
+@pytest.mark.parametrize("hidden,inter,m", [(2560, 9728, 1), (5120, 17408, 1), (2560, 9728, 2),
+                                            (2560, 9728, 4), (2560, 9728, 8), (2560, 9728, 16)])
+def test_ffn_parity(cuda, hidden, inter, m):
+    say(f"ffn H={hidden} I={inter} M={m}")
+    gup, gus, dp, ds = make_ffn(hidden, inter)
+    x = oracle.synth_activation(m, hidden, seed=7 + (m if m > 1 else 0))
+    gu = w4a16.TiledWeight.from_artifact(gup, gus, 2 * inter, hidden, pair=True, device=cuda)
+    dn = w4a16.TiledWeight.from_artifact(dp, ds, hidden, inter, device=cuda)
+    out = from_dev(w4a16.mlp_int4(to_dev(x, cuda), gu, dn))
+    ref, _, _ = oracle.ffn_bf16(x, gup, gus, dp, ds, hidden, inter)
+    assert_parity(out, ref, f"ffn H={hidden} I={inter} M={m}")
+
+
+def test_ffn_tp_slice_partial_f32(cuda):
+    """Config 4: rank 0 of tp=2 on the 27B FFN, scales kept global (reference
+    csrc/engine.cu:2308-2369: gate/up rows 0..I/2-1 of each half, down columns 0..I/2-1)."""
+    hidden, inter = 5120, 17408
+    half = inter // 2
+    say("ffn tp slice (config 4)")
+    gup, gus, dp, ds = make_ffn(hidden, inter)
+    sgp = np.concatenate([gup[:half], gup[inter:inter + half]])
+    sgs = np.concatenate([gus[:half], gus[inter:inter + half]])
+    sdp = np.ascontiguousarray(dp[:, :half // 2])
+    sds = np.ascontiguousarray(ds[:, :half // 128])
+    x = oracle.synth_activation(1, hidden, seed=7)
+    gu = w4a16.TiledWeight.from_artifact(sgp, sgs, 2 * half, hidden, pair=True, device=cuda)
+    dn = w4a16.TiledWeight.from_artifact(sdp, sds, hidden, half, device=cuda)
+    got = from_dev(w4a16.mlp_int4(to_dev(x, cuda), gu, dn, partial_f32=True))
+    ref = oracle.ffn_partial_f32(x, sgp, sgs, sdp, sds, hidden, half)
+    d = np.abs(got.astype(np.float64) - ref)
+    rel = np.linalg.norm(d) / np.linalg.norm(ref)
+    say(f"tp partial rel_l2={rel:.3g} max_abs={d.max():.3g}")
+    assert rel <= 1e-3
+    # rounded as the reference's BF16 all-reduce input would be
+    assert_parity(oracle.bf16_bits(got), oracle.bf16_bits(ref), "tp partial as BF16")
+
+
+# ---- the reference's own kernel gate, through its bridge symbol ---------------------------------
+
+def test_reference_kernel_gate_shapes():
+    rng = np.random.RandomState(11)
+    for n, k in ((256, 128), (1024, 256), (4096, 5120)):
+        w = (rng.randn(n, k) * 0.05).astype(np.float32)
+        w *= (1.0 + 0.5 * rng.rand(n, k // 128).astype(np.float32)).repeat(128, axis=1)
+        packed, scales = oracle.quantize(w)
+        deq = oracle.dequantize_numpy(packed, scales, n, k).astype(np.float64)
+        for m in (1, 2, 8, 64):
+            x = (rng.randn(m, k) * 0.5).astype(np.float32)
+            a_bits = np.ascontiguousarray(oracle.bf16_bits(x))
+            ref = bf16_f32(a_bits).astype(np.float64) @ deq.T
+            out = np.empty((m, n), np.uint16)
+            say(f"test_gemm_int4 bridge M={m} N={n} K={k}")
+            st = w4a16.lib.test_gemm_int4(out.ctypes.data, a_bits.ctypes.data, packed.ctypes.data,
+                                          scales.ctypes.data, m, n, k, 128)
+            assert st == 0, w4a16.last_error()
+            err = np.abs(bf16_f32(out).astype(np.float64) - ref)
+            scale = max(np.abs(ref).max(), 1e-9)
+            assert err.max() / scale <= 8e-3 and np.sqrt((err ** 2).mean()) / scale <= 4e-3
+            assert_parity(out, oracle.bf16_bits(ref.astype(np.float32)), f"gate M={m} {n}x{k}")
+    bad = np.zeros(128 * 192 // 2, np.uint8)
+    out = np.zeros((1, 128), np.uint16)
+    assert w4a16.lib.test_gemm_int4(out.ctypes.data, out.ctypes.data, bad.ctypes.data,
+                                    np.zeros(128, np.uint16).ctypes.data, 1, 128, 192, 128) != 0

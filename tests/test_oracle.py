@@ -1,0 +1,250 @@
+"""Pins the CPU oracle (oracle/) before anything is compared against it.
+
+Every oracle function is checked against something other than itself:
+
+* format (bf16, layout, quantize, dequantize, packed_code): the reference's known answers
+  (reference tests/quantization_format_test.c:48-245), the reference's --emit fixture and the
+  golden vectors its own quantizer/dequantizer wrote (tests/golden/), and - when oracle/_ref is
+  built here - the reference's compiled linear_weight.cpp on fresh random tensors;
+* gemm_f64 / gemm_bf16: numpy float64 matmul of numpy's own dequantization (an independent
+  library routine), plus closed forms: a one-hot activation returns a weight column exactly, a
+  zero activation returns zeros, and the product is linear in the activation;
+* silu_mul_packed: Python's math.exp at hand-picked points and the limits silu(0) = 0,
+  silu(x) -> x, silu(-x) -> 0;
+* ffn_bf16 / ffn_partial_f32: stage-by-stage recomposition from the pinned pieces above.
+"""
+
+import ctypes
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def vectors():
+    return np.load(os.path.join(GOLDEN, "quantize_vectors.npz"), allow_pickle=False)
+
+
+def golden_weights(vectors, name):
+    if f"{name}_weights_bf16" in vectors:
+        return oracle.bf16_to_f32(vectors[f"{name}_weights_bf16"])
+    if f"{name}_weights_f32bits" in vectors:
+        return vectors[f"{name}_weights_f32bits"].view(np.float32)
+    # gate cases: the reference kernel gate's frozen legacy stream (seed 11), regenerated.
+    rng = np.random.RandomState(11)
+    for n, k in ((256, 128), (1024, 256)):
+        w = (rng.randn(n, k) * 0.05).astype(np.float32)
+        w *= (1.0 + 0.5 * rng.rand(n, k // 128).astype(np.float32)).repeat(128, axis=1)
+        if name == f"gate{n}x{k}":
+            return w
+    raise KeyError(name)
+
+
+# ---- known answers (reference tests/quantization_format_test.c) --------------------------------
+
+def test_bf16_known_answers():
+    assert oracle.lib.orc_f32_to_bf16(1.0) == 0x3F80
+    assert oracle.lib.orc_f32_to_bf16(-2.0) == 0xC000
+    assert oracle.lib.orc_f32_to_bf16(0.0) == 0x0000
+    assert oracle.lib.orc_f32_to_bf16(1.0 + 2.0 ** -8) == 0x3F80        # tie -> even
+    assert oracle.lib.orc_f32_to_bf16(1.0 + 3 * 2.0 ** -8) == 0x3F82    # tie -> even (up)
+    assert oracle.lib.orc_f32_to_bf16(3.4e38) in (0x7F80, 0x7F7F)
+    assert oracle.lib.orc_bf16_to_f32(0x3F80) == 1.0
+    # numpy helper and C agree everywhere on a sweep of bit patterns
+    pats = np.arange(0, 2 ** 32, 65521, dtype=np.uint64).astype(np.uint32)
+    vals = pats.view(np.float32)
+    finite = np.isfinite(vals)
+    c = np.array([oracle.lib.orc_f32_to_bf16(float(v)) for v in vals[finite][:4000]])
+    assert np.array_equal(c, oracle.bf16_bits(vals[finite][:4000]))
+
+
+def test_layout_refusals():
+    assert oracle.layout_check(8, 128) == 0
+    assert oracle.layout_check(8, 256) == 0
+    assert oracle.layout_check(8, 192) != 0      # 1.5 groups
+    assert oracle.layout_check(12, 128) != 0     # 1.5 tiles
+    assert oracle.layout_check(0, 128) != 0
+    assert oracle.layout_check(8, -128) != 0
+    assert oracle.layout_check(8, 128, 64) != 0  # the group is the format's, not a parameter
+
+
+def test_hand_bytes_and_codes():
+    w = np.zeros((8, 128), np.float32)
+    w[0, :8] = [0, 1, -1, -7, 7, 3, -3, 2]
+    packed, scales = oracle.quantize(w)
+    assert oracle.bf16_to_f32(scales[0, 0]) == 1.0
+    assert list(packed[0, :4]) == [0x10, 0x9F, 0x37, 0x2D]
+    for k, want in enumerate([0, 1, -1, -7, 7, 3, -3, 2]):
+        assert oracle.packed_code(packed, 0, k, 128) == want
+    back = oracle.dequantize(packed, scales, 8, 128)
+    assert np.array_equal(back[0, :8], w[0, :8]) and not back[0, 8:].any()
+
+
+def test_edge_groups():
+    w = np.zeros((8, 128), np.float32)
+    packed, scales = oracle.quantize(w)
+    assert (oracle.bf16_to_f32(scales) == 1.0).all() and not packed.any()
+    w[0, 0], w[0, 1] = 0.7000001, -0.7000001
+    packed, scales = oracle.quantize(w)
+    assert oracle.packed_code(packed, 0, 0, 128) == 7
+    assert oracle.packed_code(packed, 0, 1, 128) == -7
+    w[:] = 0
+    w[0, 0] = 1e-40                                   # scale rounds to a denormal/zero: refused
+    with pytest.raises(oracle.OracleError):
+        oracle.quantize(w)
+    for bad in (np.nan, np.inf):
+        w[:] = 0
+        w[0, 5] = bad
+        with pytest.raises(oracle.OracleError):
+            oracle.quantize(w)
+    w[:] = 0
+    w[0, 0] = 0.3
+    packed, scales = oracle.quantize(w)
+    packed[0, 0] = (packed[0, 0] & 0xF0) | 0x08       # reserved code -8
+    with pytest.raises(oracle.OracleError):
+        oracle.dequantize(packed, scales, 8, 128)
+    bad_scale = scales.copy()
+    bad_scale[0, 0] = 0x0000
+    packed[0, 0] &= 0xF0
+    with pytest.raises(oracle.OracleError):
+        oracle.dequantize(packed, bad_scale, 8, 128)
+
+
+def test_requantize_fixed_point(vectors):
+    w = golden_weights(vectors, "cfgK2560")
+    p, s = oracle.quantize(w)
+    back = oracle.dequantize(p, s, *w.shape)
+    p2, s2 = oracle.quantize(back)
+    assert np.array_equal(p, p2) and np.array_equal(s, s2)
+
+
+# ---- golden vectors written by the reference's own code -----------------------------------------
+
+def test_emit_fixture():
+    with open(os.path.join(GOLDEN, "emit_fixture.json")) as handle:
+        fx = json.load(handle)
+    n, k = fx["n"], fx["k"]
+    w = np.array(fx["weights_f32_bits"], np.uint32).view(np.float32).reshape(n, k)
+    packed, scales = oracle.quantize(w)
+    assert packed.reshape(-1).tolist() == fx["packed"]
+    assert scales.reshape(-1).tolist() == fx["scales_bf16"]
+    deq = oracle.dequantize(packed, scales, n, k)
+    assert deq.view(np.uint32).reshape(-1).tolist() == fx["dequantized_f32_bits"]
+
+
+def test_golden_quantize_dequantize(vectors):
+    for name in vectors["case_names"]:
+        name = str(name)
+        w = golden_weights(vectors, name)
+        n, k = w.shape
+        packed, scales = oracle.quantize(w)
+        assert np.array_equal(packed, vectors[f"{name}_packed"]), name
+        assert np.array_equal(scales, vectors[f"{name}_scales"]), name
+        deq = oracle.dequantize(packed, scales, n, k)
+        if f"{name}_dequant_f32bits" in vectors:
+            assert np.array_equal(deq.view(np.uint32), vectors[f"{name}_dequant_f32bits"]), name
+        # the numpy restatement of the reference test's dequantizer agrees bit for bit
+        assert np.array_equal(oracle.dequantize_numpy(packed, scales, n, k).view(np.uint32),
+                              deq.view(np.uint32)), name
+
+
+@pytest.mark.skipif(oracle.ref_binary("libref_format.so") is None,
+                    reason="oracle/_ref not built (needs the reference tree)")
+def test_against_compiled_reference_random():
+    lib = ctypes.CDLL(oracle.ref_binary("libref_format.so"))
+
+    class Layout(ctypes.Structure):
+        _fields_ = [(f, ctypes.c_longlong) for f in
+                    ("n", "k", "group", "packed_bytes", "scale_count")]
+
+    rng = np.random.Generator(np.random.PCG64(99))
+    for n, k, scale in ((16, 384, 0.02), (64, 1024, 3.0), (8, 128, 1e-30)):
+        w = (rng.standard_normal((n, k)) * scale).astype(np.float32)
+        w[0, :128] = 0.0
+        lay = Layout()
+        assert lib.linear_layout_init(ctypes.byref(lay), ctypes.c_longlong(n),
+                                      ctypes.c_longlong(k), ctypes.c_longlong(128)) == 0
+        rp = np.zeros((n, k // 2), np.uint8)
+        rs = np.zeros((n, k // 128), np.uint16)
+        st = lib.linear_quantize_int4(ctypes.byref(lay), ctypes.c_void_p(w.ctypes.data),
+                                      ctypes.c_void_p(rp.ctypes.data),
+                                      ctypes.c_void_p(rs.ctypes.data))
+        if st != 0:
+            with pytest.raises(oracle.OracleError):
+                oracle.quantize(w)
+            continue
+        p, s = oracle.quantize(w)
+        assert np.array_equal(p, rp) and np.array_equal(s, rs)
+
+
+# ---- the matmul, SiLU and FFN -----------------------------------------------------------------
+
+def test_gemm_against_numpy_and_closed_forms(vectors):
+    w = golden_weights(vectors, "gate1024x256")
+    n, k = w.shape
+    p, s = vectors["gate1024x256_packed"], vectors["gate1024x256_scales"]
+    x = oracle.synth_activation(3, k, seed=5)
+    got = oracle.gemm_f64(x, p, s, n, k)
+    deq = oracle.dequantize_numpy(p, s, n, k).astype(np.float64)
+    want = oracle.bf16_to_f32(x).astype(np.float64) @ deq.T
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    # one-hot activation -> exactly the dequantized column; zero -> zeros
+    onehot = np.zeros((1, k), np.uint16)
+    onehot[0, 37] = 0x3F80
+    col = oracle.gemm_f64(onehot, p, s, n, k)[0]
+    assert np.array_equal(col, deq[:, 37])
+    assert not oracle.gemm_f64(np.zeros((1, k), np.uint16), p, s, n, k).any()
+    # linearity: x1 + x2 (both small integers, exact in BF16)
+    a = np.zeros((1, k), np.float32)
+    b = np.zeros((1, k), np.float32)
+    a[0, ::3], b[0, 1::5] = 2.0, -3.0
+    ga = oracle.gemm_f64(oracle.bf16_bits(a), p, s, n, k)
+    gb = oracle.gemm_f64(oracle.bf16_bits(b), p, s, n, k)
+    gab = oracle.gemm_f64(oracle.bf16_bits(a + b), p, s, n, k)
+    np.testing.assert_allclose(gab, ga + gb, rtol=1e-13, atol=1e-13)
+    # the BF16 variant is exactly the rounding of the FP64 one through FP32
+    gb16 = oracle.gemm_bf16(x, p, s, n, k)
+    assert np.array_equal(gb16, oracle.bf16_bits(got.astype(np.float32)))
+
+
+def test_silu_mul_points():
+    pts = [0.0, 1.0, -1.0, 2.5, -2.5, 10.0, -10.0, 30.0, -30.0, 0.125, 88.0, -88.0]
+    g = oracle.bf16_bits(np.array(pts, np.float32))
+    u = oracle.bf16_bits(np.array([1.0, 0.5, -2.0, 3.0, 1.0, 1.0, 1.0, 2.0, 2.0, -1.0, 1.0, 1.0],
+                                  np.float32))
+    inter = len(pts)
+    packed = np.concatenate([g, u])[None, :]
+    act = oracle.silu_mul_packed(packed, 1, inter)[0]
+    for i in range(inter):
+        gv, uv = float(oracle.bf16_to_f32(g[i])), float(oracle.bf16_to_f32(u[i]))
+        want = (gv / (1.0 + math.exp(-gv))) * uv
+        assert act[i] == oracle.bf16_bits(np.float32(want)), (pts[i], act[i])
+    assert act[0] == 0                                    # silu(0) = 0
+    assert oracle.bf16_to_f32(act[7]) == 60.0             # silu(30) * 2 rounds to 60
+    assert abs(float(oracle.bf16_to_f32(act[8]))) < 1e-11  # silu(-30) ~ -2.8e-12
+
+
+def test_ffn_recomposes_from_stages():
+    h, inter = 256, 384
+    wg = oracle.synth_weight(2 * inter, h, seed=1)
+    wd = oracle.synth_weight(h, inter, seed=2)
+    gp, gs = oracle.quantize(wg)
+    dp, ds = oracle.quantize(wd)
+    x = oracle.synth_activation(2, h, seed=7)
+    out, mid, act = oracle.ffn_bf16(x, gp, gs, dp, ds, h, inter)
+    assert np.array_equal(mid, oracle.gemm_bf16(x, gp, gs, 2 * inter, h))
+    assert np.array_equal(act, oracle.silu_mul_packed(mid, 2, inter))
+    assert np.array_equal(out, oracle.gemm_bf16(act, dp, ds, h, inter))
+    part = oracle.ffn_partial_f32(x, gp, gs, dp, ds, h, inter)
+    assert np.array_equal(part, oracle.gemm_f64(act, dp, ds, h, inter).astype(np.float32))
+    # the numpy CPU baseline lands within BF16 rounding of the oracle
+    base = oracle.ffn_cpu_baseline(x, gp, gs, dp, ds, h, inter)
+    d = np.abs(oracle.bf16_to_f32(base) - oracle.bf16_to_f32(out))
+    assert d.max() <= 2 ** -6 * np.abs(oracle.bf16_to_f32(out)).max()
