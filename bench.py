@@ -12,11 +12,14 @@ gate/up/SiLU kernel + down kernel) on the next set, inputs already resident in H
 (8.8 GB); ``--config 4`` its tp=2 rank-0 slice; ``--config 0`` the single K=2560, N=9728
 linear; ``--config 3`` config 1 at M = --m.
 
+Timing: the calls of one pass over the rotating sets are captured in a HIP graph and the graph
+is replayed; HIP events on the replay stream bracket the timed replays, so ``value`` is device
+time per call including the gaps between kernels, not Python's launch rate.
+
 Prints ONE JSON line. ``roofline`` is the dominant kernel's (the fused gate/up/SiLU GEMV):
 algorithmic bytes per launch (packed nibbles + BF16 scales of its weight) over its average
-duration, from HIP events recorded on the launch stream around each launch in a second timed
-pass. ``cpu_baseline`` times the CPU dequant+matmul path (numpy, BLAS) on rank 0 over a
-bounded sample.
+launch duration, from a graph holding only that kernel's launches, timed the same way.
+``cpu_baseline`` times the CPU dequant+matmul path (numpy, BLAS) over a bounded sample.
 """
 
 import argparse
@@ -160,50 +163,66 @@ def main():
     partial = args.config == 4
     out = torch.empty(m, inter if linear_only else hidden,
                       dtype=torch.float32 if partial else torch.int16, device=dev)
-    stream = torch.cuda.current_stream()
-    s_handle = stream.cuda_stream
-
-    def step(i):
-        gu, dn, _ = sets[i % count]
-        if linear_only:
-            w4a16.gemm_int4_bf16(x, gu, out, stream=s_handle)
-        else:
-            w4a16.mlp_int4(x, gu, dn, out=out, act_ws=act, partial_f32=partial, stream=s_handle)
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    start.record(stream)
-    for i in range(args.steps):
-        step(i)
-    stop.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_total = start.elapsed_time(stop)
-    us_per_call = ms_total * 1e3 / args.steps
-
-    # Second pass: events around each launch of the dominant kernel (and of the down kernel).
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     down_out = torch.empty(m, hidden, dtype=torch.int16, device=dev)
-    for i in range(args.steps):
+
+    def ffn_call(i):
         gu, dn, _ = sets[i % count]
-        e = evs[i]
-        e[0].record(stream)
         if linear_only:
-            w4a16.gemm_int4_bf16(x, gu, out, stream=s_handle)
-            e[1].record(stream)
+            w4a16.gemm_int4_bf16(x, gu, out)
         else:
-            w4a16.gate_up_silu(x, gu, act, stream=s_handle)
-            e[1].record(stream)
-            w4a16.gemm_int4_bf16(act, dn, down_out, stream=s_handle)
-        e[2].record(stream)
-    torch.cuda.synchronize()
-    k1 = sorted(e[0].elapsed_time(e[1]) * 1e3 for e in evs)
-    k2 = sorted(e[1].elapsed_time(e[2]) * 1e3 for e in evs)
-    k1_avg = sum(k1) / len(k1)
-    k2_avg = sum(k2) / len(k2)
+            w4a16.mlp_int4(x, gu, dn, out=out, act_ws=act, partial_f32=partial)
+
+    def first_kernel(i):
+        gu = sets[i % count][0]
+        if linear_only:
+            w4a16.gemm_int4_bf16(x, gu, out)
+        else:
+            w4a16.gate_up_silu(x, gu, act)
+
+    def second_kernel(i):
+        if not linear_only:
+            w4a16.gemm_int4_bf16(act, sets[i % count][1], down_out)
+
+    # Launches are captured into HIP graphs (one graph = one pass over all rotating weight sets)
+    # so the timed region measures the device, not Python's launch rate.
+    def capture(fn):
+        for i in range(count):          # eager warm-up of exactly the captured work
+            fn(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(count):
+                fn(i)
+        torch.cuda.synchronize()
+        return graph
+
+    def timed(graph, steps, warmup):
+        reps = max(1, -(-steps // count))
+        for _ in range(max(1, -(-warmup // count))):
+            graph.replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        calls = reps * count
+        return e0.elapsed_time(e1) * 1e3 / calls, wall * 1e6 / calls, calls
+
+    g_ffn = capture(ffn_call)
+    us_per_call, wall_us, calls = timed(g_ffn, args.steps, args.warmup)
+    ms_total = us_per_call * calls / 1e3
+    g_first = capture(first_kernel)
+    k1_avg, _, _ = timed(g_first, args.steps, args.warmup)
+    k2_avg = 0.0
+    if not linear_only:
+        g_second = capture(second_kernel)
+        k2_avg, _, _ = timed(g_second, args.steps, args.warmup)
+    args.steps = calls
     if linear_only:
         dom_bytes = per_set
         dom_name = "gemv_tiles_kernel<false,false> (gemm_int4_bf16)"
@@ -227,7 +246,7 @@ def main():
                    "weight_sets_rotated": count, "bytes_per_call": per_set,
                    "ffn_achieved_GBps": round(ffn_gbs, 1),
                    "ffn_frac_of_peak": round(ffn_gbs / HBM_PEAK_GBS, 4),
-                   "wall_us_per_call": round(wall * 1e6 / args.steps, 3),
+                   "wall_us_per_call": round(wall_us, 3),
                    "kernel_avg_us": {"dominant": round(k1_avg, 3), "second": round(k2_avg, 3)}},
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -3,11 +3,11 @@
  *
  * Weights are read in the tile order described in common.h. The M = 1 kernels are wave64
  * GEMVs: each lane loads one 16-byte piece (32 codes of one row) per step with a single
- * global_load_dwordx4, turns each pair of codes into a BF16 pair with one shift and one
- * and-or (value 1 + u/16, u = nibble ^ 8 = code + 8, exact in BF16), and accumulates with the
- * packed BF16 dot product v_dot2_f32_bf16 against the activation pair. Since
- * code = 16 * v - 24, a piece's contribution is 16 * dot(v, x) - 24 * sum(x), and the per-piece
- * activation sums are computed once per block when the activation is staged in LDS. The
+ * buffer_load_dwordx4, turns each pair of codes into a BF16 pair with one v_perm_b32 (value
+ * 0.5 + u/32, u = nibble ^ 8 = code + 8, exact in BF16), and accumulates with the packed BF16
+ * dot product v_dot2_f32_bf16 against the activation pair. Since code = 32 v - 24, a piece's
+ * contribution is 32 * dot(v, x) - 24 * sum(x); the per-piece activation sums are computed once
+ * per block when the activation is staged in LDS. The
  * group's BF16 scale multiplies each piece's FP32 partial (the association of the reference's
  * tiled kernel, csrc/kernels/gemm_quant.cu:130-142). Lanes of one row are reduced with
  * cross-lane shuffles; the waves of a block (split-K over groups) through LDS.
@@ -24,38 +24,40 @@ namespace {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kWaves = 4;                 /* waves per GEMV block */
-constexpr int kThreads = kWaves * 64;
-constexpr int kBatch = 4;                 /* 16-byte pieces in flight per lane */
-constexpr int kMaxGemvK = 30720;          /* activation staged in LDS: 2K bytes + sums */
+constexpr int kMaxLoads = 12;     /* 16-byte pieces in flight per lane (all of a wave's share) */
+constexpr int kMaxGemvK = 30464;  /* activation staged in LDS: 2K bytes + sums within 64 KiB */
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
                                            __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-/* BF16 pair (1 + u_lo/16, 1 + u_hi/16) for code pair q of a tile word already XORed with
- * 0x88888888 (so each nibble is u = code + 8). */
-template <int Q>
-__device__ __forceinline__ uint32_t code_pair(uint32_t w) {
-    const uint32_t shifted = (Q == 0) ? (w << 3) : (w >> (4 * Q - 3));
-    return (shifted & 0x00780078u) | 0x3F803F80u;
-}
+/* Code pairs as BF16. A tile word's low nibbles [j0, j4, j1, j5] (one per byte) and high
+ * nibbles [j2, j6, j3, j7] are moved to bits 3-6 of their bytes with the sign bit flipped
+ * (u = code + 8), and v_perm_b32 places two of them under the byte 0x3F: the BF16 value is
+ * 2^-1 * (1 + u/16) = 0.5 + u/32 = 0.75 + code/32, exact. Keeping the nibble in the top mantissa
+ * bits keeps the offset small (0.75 against a code step of 1/32), so the FP32 sums lose little
+ * to the offset that is subtracted afterwards. */
+constexpr uint32_t kMagic = 0x3F3F3F3Fu;
+constexpr uint32_t kSelLo = 0x04020400u; /* bytes 0 and 2 of the nibble word */
+constexpr uint32_t kSelHi = 0x04030401u; /* bytes 1 and 3 */
 
-/* sum_{j<32} code_j * x_j for one 16-byte piece: 16 * dot(v, x) - 24 * xsum. */
+/* sum_{j<32} code_j * x_j for one 16-byte piece: 32 * dot(v, x) - 24 * xsum. Four independent
+ * accumulators (one per dword) keep the dot-product chains short. */
 __device__ __forceinline__ float piece_dot(uint4 piece, const uint4 *xq, float xsum) {
-    float d = 0.0f;
     const uint32_t words[4] = {piece.x, piece.y, piece.z, piece.w};
+    float d[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        const uint32_t w = words[s] ^ 0x88888888u;
+        const uint32_t t = ((words[s] << 3) ^ 0x40404040u) & 0x78787878u;
+        const uint32_t t2 = ((words[s] >> 1) ^ 0x40404040u) & 0x78787878u;
         const uint4 xv = xq[s];
-        d = dot2_bf16(code_pair<0>(w), xv.x, d);
-        d = dot2_bf16(code_pair<1>(w), xv.y, d);
-        d = dot2_bf16(code_pair<2>(w), xv.z, d);
-        d = dot2_bf16(code_pair<3>(w), xv.w, d);
+        float a = dot2_bf16(__builtin_amdgcn_perm(kMagic, t, kSelLo), xv.x, 0.0f);
+        a = dot2_bf16(__builtin_amdgcn_perm(kMagic, t2, kSelLo), xv.y, a);
+        a = dot2_bf16(__builtin_amdgcn_perm(kMagic, t, kSelHi), xv.z, a);
+        d[s] = dot2_bf16(__builtin_amdgcn_perm(kMagic, t2, kSelHi), xv.w, a);
     }
-    return fmaf(16.0f, d, -24.0f * xsum);
+    return fmaf(32.0f, (d[0] + d[1]) + (d[2] + d[3]), -24.0f * xsum);
 }
 
 /* SiLU with exp computed as 2^n * 2^(r * log2 e), -g = n ln2 + r, |r| <= ln2/2 (Cody-Waite
@@ -74,108 +76,142 @@ __device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
     return bf16_rne(silu_f32(gate) * up);
 }
 
-/* One block per 8-row tile; wave w takes the group pairs w, w + kWaves, ...; half-wave h of a
- * step takes group 2*pair + h. PAIR: the tile is 4 gate + 4 up rows and the block writes four
- * BF16(silu(BF16 gate) * BF16 up) values; otherwise eight BF16 outputs (or FP32 if OUT_F32). */
-template <bool PAIR, bool OUT_F32>
-__global__ __launch_bounds__(kThreads) void gemv_tiles_kernel(
-    const uint16_t *__restrict__ x, const uint4 *__restrict__ wt,
-    const uint16_t *__restrict__ st, void *__restrict__ out, int K) {
+/* Raw buffer access: an offset past num_records reads 0 without a branch, which keeps every
+ * load of a wave unconditional (a predicated global load is compiled as a branch plus a wait). */
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return __builtin_bit_cast(uint4, v);
+}
+
+__device__ __forceinline__ uint16_t buf_load_u16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+
+constexpr uint32_t kOob = 0x80000000u; /* an offset no buffer here reaches: reads return 0 */
+
+/* A block holds TB consecutive 8-row tiles and W = TB * SK waves: wave w works on tile w / SK and
+ * takes the group pairs (w % SK) + SK * i of it; half-wave h of a step takes group 2 * pair + h.
+ * The activation loads are issued first, then every weight and scale load of the wave, so one
+ * wait covers the activation and the weights stream while it is staged into LDS.
+ * PAIR: a tile is 4 gate + 4 up rows and yields four BF16(silu(BF16 gate) x BF16 up) values;
+ * otherwise eight BF16 outputs (or FP32 if OUT_F32). */
+template <bool PAIR, bool OUT_F32, int TB, int SK>
+__global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
+    const uint16_t *__restrict__ x, const uint8_t *__restrict__ wt,
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K) {
+    constexpr int W = TB * SK;
+    /* the largest K this configuration is launched for: SK * kMaxLoads group pairs */
+    constexpr int kMaxK = (256 * kMaxLoads * SK < kMaxGemvK) ? 256 * kMaxLoads * SK : kMaxGemvK;
+    constexpr int kXIters = (kMaxK / 8 + W * 64 - 1) / (W * 64);
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
-    const int tile = blockIdx.x;
-    uint32_t *xs = reinterpret_cast<uint32_t *>(smem4);
-    float *xsum = reinterpret_cast<float *>(xs + (K >> 1));
+    const int P = (G + 1) >> 1;
+    const int tiles = N >> 3;
+    float *xsum = reinterpret_cast<float *>(smem4 + (K >> 3));
     float *red = xsum + 4 * G;
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    /* wave-uniform, made scalar so the buffer descriptors below live in SGPRs */
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = blockIdx.x * TB + wave / SK;
+    const int ks = wave % SK;
     const int half = lane >> 5;
     const int piece = lane & 31;
     const int kb = piece >> 3;
     const int r = piece & 7;
 
-    /* Issue the first batch of weight loads before staging the activation, so the HBM
-     * latency overlaps the staging. */
-    const uint4 *wtile = wt + (size_t)tile * G * 32;
-    const uint16_t *stile = st + (size_t)tile * G * 8;
-    const int pairs = (G + 1) >> 1;
-    uint4 buf[kBatch];
-    float sc[kBatch];
-    int p0 = wave;
+    /* 1. activation loads (L2-resident; the first ones to return) */
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)K * 2);
+    const int xchunks = K >> 3;
+    uint4 xv[kXIters];
 #pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-        const int g = 2 * (p0 + b * kWaves) + half;
-        const bool ok = (p0 + b * kWaves) < pairs && g < G;
-        buf[b] = ok ? wtile[(size_t)g * 32 + piece] : make_uint4(0, 0, 0, 0);
-        sc[b] = ok ? bf16_widen(stile[g * 8 + r]) : 0.0f;
+    for (int it = 0; it < kXIters; ++it) {
+        const int i = it * W * 64 + tid;
+        xv[it] = buf_load16(xr, i < xchunks ? (uint32_t)i * 16 : kOob);
     }
 
-    const uint32_t *x32 = reinterpret_cast<const uint32_t *>(x);
-    for (int i = threadIdx.x; i < (K >> 1); i += kThreads) xs[i] = x32[i];
-    __syncthreads();
-    for (int i = threadIdx.x; i < 4 * G; i += kThreads) {
-        const int g = i >> 2, b = i & 3;
-        const uint16_t *xv = reinterpret_cast<const uint16_t *>(xs) + g * 128 + 8 * b;
-        float s = 0.0f;
+    /* 2. every weight piece and scale of this wave */
+    const bool tile_ok = tile < tiles;
+    const size_t tile_bytes = (size_t)G * 512;
+    const __amdgpu_buffer_rsrc_t wr =
+        make_rsrc(wt + (size_t)(tile_ok ? tile : 0) * tile_bytes, tile_ok ? (uint32_t)tile_bytes : 0);
+    const __amdgpu_buffer_rsrc_t sr =
+        make_rsrc(st + (size_t)(tile_ok ? tile : 0) * G * 8, tile_ok ? (uint32_t)G * 16 : 0);
+    uint4 buf[kMaxLoads];
+    uint16_t sbits[kMaxLoads];
+#pragma unroll
+    for (int i = 0; i < kMaxLoads; ++i) {
+        const int p = ks + i * SK;
+        const int g = 2 * p + half;
+        const bool ok = p < P && g < G;
+        buf[i] = buf_load16(wr, ok ? (uint32_t)(g * 512 + piece * 16) : kOob);
+        sbits[i] = buf_load_u16(sr, ok ? (uint32_t)(g * 16 + r * 2) : kOob);
+    }
+
+    /* 3. stage the activation and the per-(group, kb) sums of the codes' x values */
+#pragma unroll
+    for (int it = 0; it < kXIters; ++it) {
+        const int i = it * W * 64 + tid;
+        if (i < xchunks) smem4[i] = xv[it];
+        const uint32_t w4[4] = {xv[it].x, xv[it].y, xv[it].z, xv[it].w};
+        float s8 = 0.0f;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) s += bf16_widen(xv[32 * q + j]);
-        xsum[i] = s;
+            s8 += bf16_widen((uint16_t)(w4[q] & 0xFFFFu)) + bf16_widen((uint16_t)(w4[q] >> 16));
+        /* chunk i = 16 g + 4 s + kb: add the four s of one (g, kb) */
+        s8 += __shfl_xor(s8, 4);
+        s8 += __shfl_xor(s8, 8);
+        if (i < xchunks && ((i >> 2) & 3) == 0) xsum[(i >> 4) * 4 + (i & 3)] = s8;
     }
     __syncthreads();
 
+    /* 4. dot products; a piece past the tile's groups has scale 0 (its loads read 0) and reads
+     * the activation of the last group, so it adds exactly 0 without a branch */
     float acc = 0.0f;
-    for (; p0 < pairs; p0 += kBatch * kWaves) {
-        uint4 nbuf[kBatch];
-        float nsc[kBatch];
-        const int p1 = p0 + kBatch * kWaves;
 #pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int g = 2 * (p1 + b * kWaves) + half;
-            const bool ok = (p1 + b * kWaves) < pairs && g < G;
-            nbuf[b] = ok ? wtile[(size_t)g * 32 + piece] : make_uint4(0, 0, 0, 0);
-            nsc[b] = ok ? bf16_widen(stile[g * 8 + r]) : 0.0f;
-        }
-#pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int g = 2 * (p0 + b * kWaves) + half;
-            if ((p0 + b * kWaves) < pairs && g < G) {
-                const uint4 *xq = reinterpret_cast<const uint4 *>(xs) + g * 16 + kb;
-                const uint4 xrow[4] = {xq[0], xq[4], xq[8], xq[12]};
-                acc = fmaf(piece_dot(buf[b], xrow, xsum[4 * g + kb]), sc[b], acc);
-            }
-            buf[b] = nbuf[b];
-            sc[b] = nsc[b];
+    for (int i = 0; i < kMaxLoads; ++i) {
+        if (ks + i * SK < P) { /* wave-uniform */
+            const int g = min(2 * (ks + i * SK) + half, G - 1);
+            const uint4 *xq = smem4 + g * 16 + kb;
+            const uint4 xrow[4] = {xq[0], xq[4], xq[8], xq[12]};
+            acc = fmaf(piece_dot(buf[i], xrow, xsum[4 * g + kb]), bf16_widen(sbits[i]), acc);
         }
     }
 
-    /* Lanes r, r+8, ..., r+56 hold row r's partials. */
+    /* 5. lanes r, r+8, ..., r+56 hold row r's partials; then the SK waves of a tile */
     acc += __shfl_xor(acc, 8);
     acc += __shfl_xor(acc, 16);
     acc += __shfl_xor(acc, 32);
-    if (lane < 8) red[wave * 8 + lane] = acc;
-    __syncthreads();
-    if (threadIdx.x < 8) {
-        float v = 0.0f;
+    float row_sum = acc;
+    if (SK > 1) {
+        if (lane < 8) red[wave * 8 + lane] = acc;
+        __syncthreads();
+        if (ks == 0 && lane < 8) {
+            row_sum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) v += red[w * 8 + threadIdx.x];
-        red[kWaves * 8 + threadIdx.x] = v;
-    }
-    __syncthreads();
-    if (PAIR) {
-        if (threadIdx.x < 4) {
-            const float gate = bf16_widen(bf16_rne(red[kWaves * 8 + threadIdx.x]));
-            const float up = bf16_widen(bf16_rne(red[kWaves * 8 + 4 + threadIdx.x]));
-            reinterpret_cast<uint16_t *>(out)[tile * 4 + threadIdx.x] = silu_mul_bf16(gate, up);
+            for (int w = 0; w < SK; ++w) row_sum += red[(wave + w) * 8 + lane];
         }
-    } else if (threadIdx.x < 8) {
-        const float v = red[kWaves * 8 + threadIdx.x];
+    }
+    if (ks != 0 || !tile_ok) return;
+    if (PAIR) {
+        /* lane r < 4 has gate row r, lane r + 4 the matching up row */
+        const float upv = __shfl_down(row_sum, 4);
+        if (lane < 4) {
+            const float gate = bf16_widen(bf16_rne(row_sum));
+            const float up = bf16_widen(bf16_rne(upv));
+            reinterpret_cast<uint16_t *>(out)[tile * 4 + lane] = silu_mul_bf16(gate, up);
+        }
+    } else if (lane < 8) {
         if (OUT_F32)
-            reinterpret_cast<float *>(out)[tile * 8 + threadIdx.x] = v;
+            reinterpret_cast<float *>(out)[tile * 8 + lane] = row_sum;
         else
-            reinterpret_cast<uint16_t *>(out)[tile * 8 + threadIdx.x] = bf16_rne(v);
+            reinterpret_cast<uint16_t *>(out)[tile * 8 + lane] = bf16_rne(row_sum);
     }
 }
 
@@ -277,15 +313,34 @@ int grid_for(long long work, int block) {
     return (int)(g < 1 ? 1 : g);
 }
 
-size_t gemv_smem(int K) { return (size_t)K * 2 + (size_t)(K / 128) * 16 + (kWaves + 1) * 32; }
+size_t gemv_smem(int K, int waves) {
+    return (size_t)K * 2 + (size_t)(K / 128) * 16 + (size_t)waves * 32;
+}
 
+template <bool PAIR, bool OUT_F32, int TB, int SK>
+int launch_gemv_cfg(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N,
+                    int K, hipStream_t stream) {
+    const int tiles = N / 8;
+    hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK>), dim3((tiles + TB - 1) / TB),
+                       dim3(TB * SK * 64), gemv_smem(K, TB * SK), stream, x, w, s, out, N, K);
+    return hip_status(hipGetLastError(), "gemv launch");
+}
+
+/* Split-K: the smallest power of two keeping a wave at <= kMaxLoads pieces; tiles per block
+ * then fill four waves where the split leaves room. */
 template <bool PAIR, bool OUT_F32>
 int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N, int K,
                 hipStream_t stream) {
-    const size_t smem = gemv_smem(K);
-    hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32>), dim3(N / 8), dim3(kThreads), smem,
-                       stream, x, reinterpret_cast<const uint4 *>(w), s, out, K);
-    return hip_status(hipGetLastError(), "gemv launch");
+    const int pairs = (K / 128 + 1) / 2;
+    int sk = 1;
+    while (sk < 16 && (pairs + sk - 1) / sk > kMaxLoads) sk *= 2;
+    switch (sk) {
+        case 1: return launch_gemv_cfg<PAIR, OUT_F32, 4, 1>(x, w, s, out, N, K, stream);
+        case 2: return launch_gemv_cfg<PAIR, OUT_F32, 2, 2>(x, w, s, out, N, K, stream);
+        case 4: return launch_gemv_cfg<PAIR, OUT_F32, 1, 4>(x, w, s, out, N, K, stream);
+        case 8: return launch_gemv_cfg<PAIR, OUT_F32, 1, 8>(x, w, s, out, N, K, stream);
+        default: return launch_gemv_cfg<PAIR, OUT_F32, 1, 16>(x, w, s, out, N, K, stream);
+    }
 }
 
 /* Shape refusals of the reference wrapper (csrc/kernels/gemm_quant.cu:204-231), plus the

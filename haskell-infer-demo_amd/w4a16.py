@@ -80,6 +80,12 @@ def header_symbols():
 
 
 def load_library(path=LIB_PATH):
+    # torch ships its own libamdhip64.so.7; loading it first makes this library bind to the same
+    # HIP runtime instead of /opt/rocm's, so torch tensors and these kernels share one runtime.
+    try:
+        import torch  # noqa: F401
+    except ImportError:  # pragma: no cover - torch-free callers use the system runtime
+        pass
     if not os.path.exists(path):
         raise ImportError(f"libw4a16.so is not built ({path}); run __graft_entry__.build()")
     lib = ctypes.CDLL(path)

@@ -30,28 +30,29 @@ def bf16_f32(bits):
     return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
-def parity_metrics(got_bits, ref, ref_is_bits=True):
+def parity_metrics(got_bits, ref, ref_is_bits=True, floor_div=64.0):
     """Compare BF16 outputs with the oracle.
 
     rel_l2: ||got - ref|| / ||ref|| over the whole output.
-    max_ulp: max |got - ref| in BF16 ULPs of max(|ref|, rms(ref)/64). Below rms/64 the FP32
-    accumulation error of any FP32-accumulated kernel (the reference's included) is itself of
-    the order of a BF16 ULP of the element, so the ULP there is taken at that floor.
+    max_ulp: max |got - ref| in BF16 ULPs of max(|ref|, rms(ref)/floor_div) (default 64). Near
+    zero an element's own ULP is far below the FP32 accumulation error of any FP32-accumulated
+    kernel (the reference's included), so the ULP there is taken at that floor.
     """
     got = bf16_f32(got_bits).astype(np.float64)
     r = bf16_f32(ref).astype(np.float64) if ref_is_bits else np.asarray(ref, np.float64)
     diff = np.abs(got - r)
     rel_l2 = float(np.linalg.norm(diff) / max(np.linalg.norm(r), 1e-30))
     rms = float(np.sqrt(np.mean(r * r))) if r.size else 0.0
-    mag = np.maximum(np.abs(r), rms / 64.0)
+    mag = np.maximum(np.abs(r), rms / floor_div)
     ulp = np.exp2(np.floor(np.log2(np.maximum(mag, 1e-38))) - 7)
     ulps = diff / ulp
     return {"rel_l2": rel_l2, "max_ulp": float(ulps.max()) if ulps.size else 0.0,
             "n_over_1ulp": int((ulps > 1.0).sum()), "n": int(r.size)}
 
 
-def assert_parity(got_bits, ref, what, rel_l2=1e-3, max_ulp=2.0, ref_is_bits=True):
-    m = parity_metrics(got_bits, ref, ref_is_bits)
+def assert_parity(got_bits, ref, what, rel_l2=1e-3, max_ulp=2.0, ref_is_bits=True,
+                  floor_div=64.0):
+    m = parity_metrics(got_bits, ref, ref_is_bits, floor_div)
     print(f"{what}: rel_l2={m['rel_l2']:.3g} max_ulp={m['max_ulp']:.3g} "
           f">1ulp={m['n_over_1ulp']}/{m['n']}", flush=True)
     assert m["rel_l2"] <= rel_l2, (what, m)
