@@ -3,9 +3,9 @@
  *
  * Weights are read in the tile order described in common.h. The M = 1 kernels are wave64
  * GEMVs: each lane loads one 16-byte piece (32 codes of one row) per step with a single
- * buffer_load_dwordx4, turns each pair of codes into a BF16 pair with one v_perm_b32 (value
- * 0.5 + u/32, u = nibble ^ 8 = code + 8, exact in BF16), and accumulates with the packed BF16
- * dot product v_dot2_f32_bf16 against the activation pair. Since code = 32 v - 24, a piece's
+ * buffer_load_dwordx4, turns each pair of codes into a BF16 pair with a shift and one
+ * v_bitop3_b32 (value 0.5 + u/32, u = nibble ^ 8 = code + 8, exact in BF16), and accumulates with
+ * the packed BF16 dot product v_dot2_f32_bf16 against the activation pair. Since code = 32 v - 24, a piece's
  * contribution is 32 * dot(v, x) - 24 * sum(x); the per-piece activation sums are computed once
  * per block when the activation is staged in LDS. The
  * group's BF16 scale multiplies each piece's FP32 partial (the association of the reference's
@@ -14,7 +14,9 @@
  */
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
+#include <mutex>
 
 #include "common.h"
 
@@ -32,32 +34,32 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                            __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-/* Code pairs as BF16. A tile word's low nibbles [j0, j4, j1, j5] (one per byte) and high
- * nibbles [j2, j6, j3, j7] are moved to bits 3-6 of their bytes with the sign bit flipped
- * (u = code + 8), and v_perm_b32 places two of them under the byte 0x3F: the BF16 value is
- * 2^-1 * (1 + u/16) = 0.5 + u/32 = 0.75 + code/32, exact. Keeping the nibble in the top mantissa
- * bits keeps the offset small (0.75 against a code step of 1/32), so the FP32 sums lose little
- * to the offset that is subtracted afterwards. */
-constexpr uint32_t kMagic = 0x3F3F3F3Fu;
-constexpr uint32_t kSelLo = 0x04020400u; /* bytes 0 and 2 of the nibble word */
-constexpr uint32_t kSelHi = 0x04030401u; /* bytes 1 and 3 */
+/* Code pairs as BF16. In a tile word the pair (j = 2q, 2q+1) sits at bits 4q and 16 + 4q, so one
+ * shift puts both nibbles at bits 3-6 of their 16-bit halves and one v_bitop3_b32 computes
+ * (s & 0x00780078) ^ 0x3F403F40: it keeps the two nibbles, flips their sign bits (u = code + 8)
+ * and sets the exponent byte 0x3F (the mask and the constant are disjoint but for the sign bits).
+ * The BF16 value is 2^-1 * (1 + u/16) = 0.5 + u/32 = 0.75 + code/32, exact. Keeping the nibble in
+ * the top mantissa bits keeps the offset small (0.75 against a code step of 1/32), so the FP32
+ * sums lose little to the offset that is subtracted afterwards. */
+__device__ __forceinline__ uint32_t code_pair(uint32_t shifted) {
+    return (shifted & 0x00780078u) ^ 0x3F403F40u;
+}
 
-/* sum_{j<32} code_j * x_j for one 16-byte piece: 32 * dot(v, x) - 24 * xsum. Four independent
- * accumulators (one per dword) keep the dot-product chains short. */
+/* sum_{j<32} code_j * x_j for one 16-byte piece: 32 * dot(v, x) - 24 * xsum (one dependent
+ * v_dot2 chain: the accumulator forwards, so splitting it only adds combining work). */
 __device__ __forceinline__ float piece_dot(uint4 piece, const uint4 *xq, float xsum) {
     const uint32_t words[4] = {piece.x, piece.y, piece.z, piece.w};
-    float d[4];
+    float a = 0.0f;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        const uint32_t t = ((words[s] << 3) ^ 0x40404040u) & 0x78787878u;
-        const uint32_t t2 = ((words[s] >> 1) ^ 0x40404040u) & 0x78787878u;
+        const uint32_t w = words[s];
         const uint4 xv = xq[s];
-        float a = dot2_bf16(__builtin_amdgcn_perm(kMagic, t, kSelLo), xv.x, 0.0f);
-        a = dot2_bf16(__builtin_amdgcn_perm(kMagic, t2, kSelLo), xv.y, a);
-        a = dot2_bf16(__builtin_amdgcn_perm(kMagic, t, kSelHi), xv.z, a);
-        d[s] = dot2_bf16(__builtin_amdgcn_perm(kMagic, t2, kSelHi), xv.w, a);
+        a = dot2_bf16(code_pair(w << 3), xv.x, a);
+        a = dot2_bf16(code_pair(w >> 1), xv.y, a);
+        a = dot2_bf16(code_pair(w >> 5), xv.z, a);
+        a = dot2_bf16(code_pair(w >> 9), xv.w, a);
     }
-    return fmaf(32.0f, (d[0] + d[1]) + (d[2] + d[3]), -24.0f * xsum);
+    return fmaf(32.0f, a, -24.0f * xsum);
 }
 
 /* SiLU with exp computed as 2^n * 2^(r * log2 e), -g = n ln2 + r, |r| <= ln2/2 (Cody-Waite
@@ -215,6 +217,195 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
     }
 }
 
+/* ------------------------------------------------------------------------------------------
+ * MFMA form (M = 1..16 activation rows): v_mfma_f32_16x16x32_bf16 with the activation as the A
+ * operand (lane l holds row l % 16, k-block l / 16) and sixteen weight rows as B (lane l holds
+ * weight row l % 16 of a tile pair, the same k-block): lanes 0-7 carry tile 2p, lanes 8-15 tile
+ * 2p + 1, and lane l's 16-byte piece (kb = l / 16, r = l % 8) supplies one MFMA per dword, so a
+ * group of one tile pair is four MFMAs and the matrix core, not the VALU, does the FMAs. Only
+ * the rows < M of A are non-zero. B holds v = 0.75 + code/32 (see the unpack above) and the group
+ * result is 32 * D - 24 * X with X the group's activation sum. Each wave owns one tile pair over
+ * the block's K range (GS groups, all loads issued up front); the four waves of a block share the
+ * staged activation of that range. When K is split over S blocks, every block writes its FP32
+ * partial and the last one to arrive on a tile pair (device-scope counter) sums the S partials in
+ * split order - the result does not depend on arrival order - and resets the counter.
+ * ---------------------------------------------------------------------------------------- */
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kGMax = 20;       /* groups per wave (16-byte loads in flight per lane) */
+constexpr int kMfmaWaves = 4;   /* tile pairs per block */
+enum { kOutBf16 = 0, kOutPairSilu = 1, kOutF32 = 2 };
+
+__device__ __forceinline__ bf16x8_t unpack8(uint32_t word) {
+    uint4 v;
+    v.x = code_pair(word << 3);
+    v.y = code_pair(word >> 1);
+    v.z = code_pair(word >> 5);
+    v.w = code_pair(word >> 9);
+    return __builtin_bit_cast(bf16x8_t, v);
+}
+
+template <int OUT, int XPRE>
+__global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
+    const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, int S, int GS,
+    float *__restrict__ partial, unsigned *__restrict__ counters) {
+    extern __shared__ uint4 smem4[];
+    const int G = K >> 7;
+    const int tiles = N >> 3;
+    const int NT = (tiles + 1) >> 1;
+    const int ks = blockIdx.x % S;
+    const int g0 = ks * GS;
+    const int ng = min(GS, G - g0);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tp = (int)(blockIdx.x / S) * kMfmaWaves + wave;
+    const int n = lane & 15;
+    const int q = lane >> 4;
+    const int tile = 2 * tp + (n >> 3);
+    const int r = n & 7;
+
+    /* 1. the activation chunks of this block's K range (8 BF16 each; row m, chunk c) */
+    const int cpr = ng * 16;            /* chunks per activation row */
+    const int chunks = M * cpr;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)M * K * 2);
+    uint4 xv[XPRE];
+#pragma unroll
+    for (int it = 0; it < XPRE; ++it) {
+        const int i = it * kMfmaWaves * 64 + tid;
+        const int m = i / cpr, c = i - m * cpr;
+        xv[it] = buf_load16(xr, i < chunks ? (uint32_t)((m * K + g0 * 128 + c * 8) * 2) : kOob);
+    }
+
+    /* 2. every weight piece and scale of this wave's tile pair and K range */
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wt, (uint32_t)((size_t)N * K / 2));
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(st, (uint32_t)((size_t)N * G * 2));
+    const bool tile_ok = tp < NT && tile < tiles;
+    uint4 buf[kGMax];
+    uint16_t sbits[kGMax];
+#pragma unroll
+    for (int i = 0; i < kGMax; ++i) {
+        const bool ok = tile_ok && i < ng;
+        const uint32_t unit = (uint32_t)(tile * G + g0 + i);
+        buf[i] = buf_load16(wr, ok ? (unit * 32 + q * 8 + r) * 16 : kOob);
+        sbits[i] = buf_load_u16(sr, ok ? (unit * 8 + r) * 2 : kOob);
+    }
+
+    /* 3. stage the activation (row-major [M][ng*128] BF16) and the group sums X[m][g] */
+    float *xsum = reinterpret_cast<float *>(smem4 + chunks);
+    auto stage = [&](int i, uint4 v) {
+        if (i < chunks) smem4[i] = v;
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+        float s8 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            s8 += bf16_widen((uint16_t)(w4[j] & 0xFFFFu)) + bf16_widen((uint16_t)(w4[j] >> 16));
+        /* 16 consecutive chunks make one group of one row */
+        s8 += __shfl_xor(s8, 1);
+        s8 += __shfl_xor(s8, 2);
+        s8 += __shfl_xor(s8, 4);
+        s8 += __shfl_xor(s8, 8);
+        if (i < chunks && (i & 15) == 0) xsum[i >> 4] = s8;
+    };
+#pragma unroll
+    for (int it = 0; it < XPRE; ++it) stage(it * kMfmaWaves * 64 + tid, xv[it]);
+    for (int i0 = XPRE * kMfmaWaves * 64; i0 < chunks; i0 += kMfmaWaves * 64) {
+        const int i = i0 + tid;
+        const int m = i / cpr, c = i - m * cpr;
+        stage(i, buf_load16(xr, i < chunks ? (uint32_t)((m * K + g0 * 128 + c * 8) * 2) : kOob));
+    }
+    __syncthreads();
+    if (tp >= NT) return;
+
+    /* 4. four MFMAs per group, then scale and offset correction into acc[i] (row 4q + i) */
+    const int arow = min(n, M - 1);
+    const bool a_live = n < M;
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int gl = 0; gl < kGMax; ++gl) {
+        if (gl < ng) { /* block-uniform */
+            const uint32_t words[4] = {buf[gl].x, buf[gl].y, buf[gl].z, buf[gl].w};
+            const uint4 *xa = smem4 + arow * cpr + gl * 16 + q;
+            f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                uint4 av = xa[4 * s];
+                if (!a_live) av = make_uint4(0, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
+                                                            unpack8(words[s]), d, 0, 0, 0);
+            }
+            const float sc = bf16_widen(sbits[gl]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = min(4 * q + i, M - 1);
+                acc[i] = fmaf(sc, fmaf(32.0f, d[i], -24.0f * xsum[m * ng + gl]), acc[i]);
+            }
+        }
+    }
+
+    /* 5. split-K combine: publish, count, and let the last arrival sum in split order. The
+     * partials and the counter are accessed with agent-scope atomics (coherent across the XCDs'
+     * L2 caches), and the wave waits for its partial stores to complete before it counts, so
+     * whoever reads count S - 1 sees every partial; no cache-wide fence is needed. */
+    if (S > 1) {
+        float *mine = partial + ((size_t)ks * NT + tp) * 16 * M;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (4 * q + i < M)
+                __hip_atomic_store(mine + (4 * q + i) * 16 + n, acc[i], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        unsigned prev = 0;
+        if (lane == 0)
+            prev = __hip_atomic_fetch_add(&counters[tp], 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+        prev = __shfl(prev, 0);
+        if (prev != (unsigned)(S - 1)) return;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = 0.0f;
+        for (int k2 = 0; k2 < S; ++k2) {
+            const float *src = partial + ((size_t)k2 * NT + tp) * 16 * M;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (4 * q + i < M)
+                    acc[i] += __hip_atomic_load(src + (4 * q + i) * 16 + n, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (lane == 0)
+            __hip_atomic_store(&counters[tp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    /* 6. epilogue */
+    if (OUT == kOutPairSilu) {
+        const int inter = N >> 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float upv = __shfl_down(acc[i], 4);
+            const int m = 4 * q + i;
+            if (r < 4 && m < M && tile < tiles) {
+                const float gate = bf16_widen(bf16_rne(acc[i]));
+                const float up = bf16_widen(bf16_rne(upv));
+                reinterpret_cast<uint16_t *>(out)[(size_t)m * inter + tile * 4 + r] =
+                    silu_mul_bf16(gate, up);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * q + i;
+            if (m < M && tile < tiles) {
+                const size_t o = (size_t)m * N + tile * 8 + r;
+                if (OUT == kOutF32)
+                    reinterpret_cast<float *>(out)[o] = acc[i];
+                else
+                    reinterpret_cast<uint16_t *>(out)[o] = bf16_rne(acc[i]);
+            }
+        }
+    }
+}
+
 __global__ void silu_mul_packed_kernel(uint16_t *__restrict__ out,
                                        const uint16_t *__restrict__ packed, int tokens,
                                        int inter) {
@@ -327,7 +518,7 @@ int launch_gemv_cfg(const uint16_t *x, const uint8_t *w, const uint16_t *s, void
 }
 
 /* Split-K: the smallest power of two keeping a wave at <= kMaxLoads pieces; tiles per block
- * then fill four waves where the split leaves room. */
+ * (measured on MI355X) keep 4-8 waves per block. */
 template <bool PAIR, bool OUT_F32>
 int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N, int K,
                 hipStream_t stream) {
@@ -337,9 +528,112 @@ int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *ou
     switch (sk) {
         case 1: return launch_gemv_cfg<PAIR, OUT_F32, 4, 1>(x, w, s, out, N, K, stream);
         case 2: return launch_gemv_cfg<PAIR, OUT_F32, 2, 2>(x, w, s, out, N, K, stream);
-        case 4: return launch_gemv_cfg<PAIR, OUT_F32, 1, 4>(x, w, s, out, N, K, stream);
+        case 4: return launch_gemv_cfg<PAIR, OUT_F32, 2, 4>(x, w, s, out, N, K, stream);
         case 8: return launch_gemv_cfg<PAIR, OUT_F32, 1, 8>(x, w, s, out, N, K, stream);
         default: return launch_gemv_cfg<PAIR, OUT_F32, 1, 16>(x, w, s, out, N, K, stream);
+    }
+}
+
+/* Split-K scratch for the MFMA form: FP32 partials and per-tile-pair arrival counters, one set
+ * per device, grown on demand (growth synchronises the device; counters are zeroed when
+ * allocated and every kernel leaves them zero). Calls that overlap in time on one device share
+ * it, so they must be ordered on one stream. */
+struct SplitScratch {
+    float *partial = nullptr;
+    size_t partial_bytes = 0;
+    unsigned *counters = nullptr;
+    size_t ncounters = 0;
+};
+std::mutex g_scratch_mu;
+SplitScratch g_scratch[64];
+
+int split_scratch(size_t partial_bytes, size_t ncounters, float **partial, unsigned **counters) {
+    int dev = 0;
+    int st = hip_status(hipGetDevice(&dev), "hipGetDevice");
+    if (st) return st;
+    if (dev < 0 || dev >= 64) return set_error(W4A16_ERR_CONFIG, "device ordinal %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    SplitScratch &sc = g_scratch[dev];
+    if (sc.partial_bytes < partial_bytes) {
+        size_t want = (size_t)4 << 20;
+        while (want < partial_bytes) want *= 2;
+        if (sc.partial) (void)hipFree(sc.partial);
+        sc.partial = nullptr;
+        sc.partial_bytes = 0;
+        if (hipMalloc((void **)&sc.partial, want) != hipSuccess)
+            return set_error(W4A16_ERR_ALLOC, "split-K scratch: hipMalloc(%zu) failed", want);
+        sc.partial_bytes = want;
+    }
+    if (sc.ncounters < ncounters) {
+        size_t want = 65536;
+        while (want < ncounters) want *= 2;
+        if (sc.counters) (void)hipFree(sc.counters);
+        sc.counters = nullptr;
+        sc.ncounters = 0;
+        if (hipMalloc((void **)&sc.counters, want * sizeof(unsigned)) != hipSuccess)
+            return set_error(W4A16_ERR_ALLOC, "split-K counters: hipMalloc failed");
+        st = hip_status(hipMemset(sc.counters, 0, want * sizeof(unsigned)), "hipMemset counters");
+        if (!st) st = hip_status(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        if (st) return st;
+        sc.ncounters = want;
+    }
+    *partial = sc.partial;
+    *counters = sc.counters;
+    return W4A16_OK;
+}
+
+struct MfmaPlan {
+    int S, GS, xpre, grid;
+    size_t smem, partial_bytes, ncounters;
+};
+
+/* K split: at most kGMax groups per wave, activation range within 32 KiB of LDS, and enough
+ * blocks that the waves cover the chip several times over. */
+MfmaPlan plan_mfma(int M, int N, int K) {
+    MfmaPlan p{};
+    const int G = K / 128;
+    const int NT = (N / 8 + 1) / 2;
+    const int gmax = std::max(1, std::min(kGMax, 128 / M));
+    int S = (G + gmax - 1) / gmax;
+    const int nblk = (NT + kMfmaWaves - 1) / kMfmaWaves;
+    while ((long long)nblk * kMfmaWaves * S < 1024 && (G + S) / (S + 1) >= 4) ++S;
+    p.GS = (G + S - 1) / S;
+    p.S = (G + p.GS - 1) / p.GS;
+    const int chunks = M * p.GS * 16;
+    const int pre = (chunks + kMfmaWaves * 64 - 1) / (kMfmaWaves * 64);
+    p.xpre = pre <= 1 ? 1 : pre <= 2 ? 2 : pre <= 4 ? 4 : 8;
+    p.grid = nblk * p.S;
+    p.smem = (size_t)chunks * 16 + (size_t)M * p.GS * 4;
+    p.partial_bytes = p.S > 1 ? (size_t)p.S * NT * 16 * M * 4 : 0;
+    p.ncounters = p.S > 1 ? (size_t)NT : 0;
+    return p;
+}
+
+template <int OUT, int XPRE>
+int launch_mfma_x(const MfmaPlan &p, const uint16_t *x, int M, const uint8_t *w,
+                  const uint16_t *s, void *out, int N, int K, float *partial, unsigned *counters,
+                  hipStream_t stream) {
+    hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE>), dim3(p.grid), dim3(kMfmaWaves * 64), p.smem,
+                       stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters);
+    return hip_status(hipGetLastError(), "mfma gemm launch");
+}
+
+/* M <= 16 rows of x against a tile-order weight. */
+template <int OUT>
+int launch_mfma(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
+                int K, hipStream_t stream) {
+    const MfmaPlan p = plan_mfma(M, N, K);
+    float *partial = nullptr;
+    unsigned *counters = nullptr;
+    if (p.S > 1) {
+        int st = split_scratch(p.partial_bytes, p.ncounters, &partial, &counters);
+        if (st) return st;
+    }
+    switch (p.xpre) {
+        case 1: return launch_mfma_x<OUT, 1>(p, x, M, w, s, out, N, K, partial, counters, stream);
+        case 2: return launch_mfma_x<OUT, 2>(p, x, M, w, s, out, N, K, partial, counters, stream);
+        case 4: return launch_mfma_x<OUT, 4>(p, x, M, w, s, out, N, K, partial, counters, stream);
+        default: return launch_mfma_x<OUT, 8>(p, x, M, w, s, out, N, K, partial, counters, stream);
     }
 }
 
@@ -375,17 +669,31 @@ int check_gemm_args(const void *a, const void *p, const void *s, const void *o, 
 /* C ABI                                                                                     */
 /* ---------------------------------------------------------------------------------------- */
 
+/* Rows of x: M = 1 takes the v_dot2 GEMV; 2 <= M <= 16 the MFMA form (one pass over the weight
+ * for all rows); larger M runs the MFMA form on 16-row slices. */
+template <int OUT>
+static int run_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
+                    int N, int K, hipStream_t stream) {
+    constexpr bool PAIR = OUT == kOutPairSilu;
+    constexpr bool F32 = OUT == kOutF32;
+    const int out_cols = PAIR ? N / 2 : N;
+    const size_t out_elem = F32 ? 4 : 2;
+    for (int m0 = 0; m0 < M; m0 += 16) {
+        const int rows = std::min(16, M - m0);
+        const uint16_t *xs = x + (size_t)m0 * K;
+        void *os = static_cast<char *>(out) + (size_t)m0 * out_cols * out_elem;
+        const int st = rows == 1 ? launch_gemv<PAIR, F32>(xs, w, s, os, N, K, stream)
+                                 : launch_mfma<OUT>(xs, rows, w, s, os, N, K, stream);
+        if (st) return st;
+    }
+    return W4A16_OK;
+}
+
 extern "C" int gemm_int4_bf16(const uint16_t *a, const uint8_t *packed, const uint16_t *scales,
                               uint16_t *out, int M, int N, int K, int group, void *stream) {
     int st = check_gemm_args(a, packed, scales, out, M, N, K, group, "gemm_int4_bf16");
     if (st) return st > 0 ? W4A16_OK : st;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    for (int m = 0; m < M; ++m) {
-        st = launch_gemv<false, false>(a + (size_t)m * K, packed, scales, out + (size_t)m * N, N,
-                                       K, s);
-        if (st) return st;
-    }
-    return W4A16_OK;
+    return run_rows<kOutBf16>(a, M, packed, scales, out, N, K, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int gate_up_silu_int4_bf16(const uint16_t *x, const uint8_t *gu_packed,
@@ -395,13 +703,8 @@ extern "C" int gate_up_silu_int4_bf16(const uint16_t *x, const uint8_t *gu_packe
     int st = check_gemm_args(x, gu_packed, gu_scales, act, M, 2 * inter, hidden, W4A16_GROUP,
                              "gate_up_silu_int4_bf16");
     if (st) return st > 0 ? W4A16_OK : st;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    for (int m = 0; m < M; ++m) {
-        st = launch_gemv<true, false>(x + (size_t)m * hidden, gu_packed, gu_scales,
-                                      act + (size_t)m * inter, 2 * inter, hidden, s);
-        if (st) return st;
-    }
-    return W4A16_OK;
+    return run_rows<kOutPairSilu>(x, M, gu_packed, gu_scales, act, 2 * inter, hidden,
+                                  static_cast<hipStream_t>(stream));
 }
 
 static int mlp_common(const uint16_t *normed, const uint8_t *gup, const uint16_t *gus,
@@ -417,16 +720,8 @@ static int mlp_common(const uint16_t *normed, const uint8_t *gup, const uint16_t
     st = gate_up_silu_int4_bf16(normed, gup, gus, act, M, hidden, inter, stream);
     if (st) return st;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    for (int m = 0; m < M; ++m) {
-        st = out_f32 ? launch_gemv<false, true>(act + (size_t)m * inter, dnp, dns,
-                                                static_cast<float *>(out) + (size_t)m * hidden,
-                                                hidden, inter, s)
-                     : launch_gemv<false, false>(act + (size_t)m * inter, dnp, dns,
-                                                 static_cast<uint16_t *>(out) + (size_t)m * hidden,
-                                                 hidden, inter, s);
-        if (st) return st;
-    }
-    return W4A16_OK;
+    return out_f32 ? run_rows<kOutF32>(act, M, dnp, dns, out, hidden, inter, s)
+                   : run_rows<kOutBf16>(act, M, dnp, dns, out, hidden, inter, s);
 }
 
 extern "C" int mlp_int4_bf16(const uint16_t *normed, const uint8_t *gup, const uint16_t *gus,
