@@ -1,0 +1,287 @@
+/*
+ * engine.cpp - The dense-FFN INT4 operand store behind engine_load_quantized_ffn, and the
+ * decode-time FFN dispatch that reads it.
+ *
+ * An EngineHandle here carries what the loader needs from the reference engine's descriptor
+ * (layer count, which layers are dense, hidden and intermediate sizes, the tensor-parallel
+ * degree and this handle's rank, the device) and owns the device operands of every dense layer.
+ * engine_load_quantized_ffn follows reference csrc/engine.cu:2207-2428:
+ *   - parse and validate weights.manifest.json;
+ *   - refuse expert parallelism, a sidecar that does not cover every dense layer with an
+ *     mlpGateUp pair and an mlpDown entry, and shapes that are not the checkpoint's;
+ *   - slice this rank's rows (gate/up: out_dim) and columns (down: in_dim) exactly as the
+ *     reference's slice_rows does, keeping the global scales, and refuse a column split that is
+ *     not on a 128-wide group boundary;
+ *   - read each artifact with its size, dtype and SHA-256 checked;
+ *   - upload, then re-lay into tile order on the device (a permutation; the artifact is never
+ *     re-quantized).
+ * Loading is all-or-nothing: on any refusal every buffer this call allocated is freed and the
+ * handle keeps what it had. Every failure after argument checking returns W4A16_ERR_WEIGHTS
+ * with the reason in engine_last_error(), as the reference's catch-all does (engine.cu:2423-2427).
+ */
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <memory>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "loader.h"
+
+using namespace w4a16;
+
+namespace {
+
+struct DevBuf {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf &) = delete;
+    DevBuf &operator=(const DevBuf &) = delete;
+    DevBuf(DevBuf &&o) noexcept : ptr(o.ptr), bytes(o.bytes) { o.ptr = nullptr; o.bytes = 0; }
+    DevBuf &operator=(DevBuf &&o) noexcept {
+        if (this != &o) { release(); ptr = o.ptr; bytes = o.bytes; o.ptr = nullptr; o.bytes = 0; }
+        return *this;
+    }
+    ~DevBuf() { release(); }
+    void release() {
+        if (ptr) (void)hipFree(ptr);
+        ptr = nullptr;
+        bytes = 0;
+    }
+    int alloc(size_t n) {
+        release();
+        if (hipMalloc(&ptr, n) != hipSuccess) {
+            ptr = nullptr;
+            return set_error(W4A16_ERR_ALLOC, "hipMalloc(%zu) failed", n);
+        }
+        bytes = n;
+        return W4A16_OK;
+    }
+};
+
+struct LayerOperands {
+    bool loaded = false;
+    DevBuf gu_packed, gu_scales, dn_packed, dn_scales; /* tile order */
+};
+
+}  // namespace
+
+struct EngineHandle {
+    W4A16EngineConfig cfg;
+    std::vector<unsigned char> dense;
+    int local_inter = 0; /* intermediate columns this rank holds */
+    std::vector<LayerOperands> layers;
+    DevBuf act_ws;       /* [max_tokens, local_inter] BF16 */
+    int quantized_layers = 0;
+};
+
+namespace {
+
+std::string join_error(const char *prefix) {
+    std::string s = prefix;
+    s += w4a16_last_error();
+    return s;
+}
+
+/* rows [row_off, row_off + rows) of a row-major [*, row_bytes_src] buffer, bytes
+ * [col_byte, col_byte + row_bytes) of each (reference csrc/engine.cu:2194-2205). */
+void slice_rows(uint8_t *dst, const uint8_t *src, long long src_row_bytes, long long row_off,
+                long long rows, long long col_byte, long long row_bytes) {
+    for (long long i = 0; i < rows; ++i)
+        std::memcpy(dst + i * row_bytes, src + (row_off + i) * src_row_bytes + col_byte, (size_t)row_bytes);
+}
+
+/* Upload an artifact-layout weight and re-lay it into tile order in `packed` / `scales`. */
+int upload_tiled(const std::vector<uint8_t> &p, const std::vector<uint8_t> &s, long long n,
+                 long long k, int pair, DevBuf *packed, DevBuf *scales) {
+    DevBuf sp, ss;
+    int st = sp.alloc(p.size());
+    if (!st) st = ss.alloc(s.size());
+    if (!st) st = packed->alloc(p.size());
+    if (!st) st = scales->alloc(s.size());
+    if (st) return st;
+    if (hipMemcpy(sp.ptr, p.data(), p.size(), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(ss.ptr, s.data(), s.size(), hipMemcpyHostToDevice) != hipSuccess)
+        return set_error(W4A16_ERR_HIP, "upload of INT4 operands failed");
+    st = w4a16_tile_pack_device(n, k, pair, static_cast<const uint8_t *>(sp.ptr),
+                                static_cast<const uint16_t *>(ss.ptr),
+                                static_cast<uint8_t *>(packed->ptr),
+                                static_cast<uint16_t *>(scales->ptr), nullptr);
+    if (st) return st;
+    if (hipDeviceSynchronize() != hipSuccess) return set_error(W4A16_ERR_HIP, "re-layout failed");
+    return W4A16_OK;
+}
+
+int read_text(const std::string &path, std::string *out) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) return set_error(W4A16_ERR_WEIGHTS, "cannot open %s", path.c_str());
+    std::stringstream ss;
+    ss << f.rdbuf();
+    *out = ss.str();
+    return W4A16_OK;
+}
+
+int load_impl(EngineHandle *eng, const std::string &root) {
+    const W4A16EngineConfig &c = eng->cfg;
+    std::string json;
+    int st = read_text(root + "/weights.manifest.json", &json);
+    if (st) return st;
+    Manifest m;
+    if (manifest_parse(json, &m) != kManifestOk) return W4A16_ERR_WEIGHTS;
+    if (c.ep_size > 1)
+        return set_error(W4A16_ERR_WEIGHTS, "the converter quantizes whole tensors and no expert role is "
+                         "admitted, so a quantized expert-parallel engine is refused");
+    int dense = 0, covered = 0;
+    for (int l = 0; l < c.num_layers; ++l) {
+        if (!eng->dense[l]) continue;
+        ++dense;
+        if (m.find_pair("mlpGateUp", l) >= 0 && m.find_entry(l, "mlpDown") >= 0) ++covered;
+    }
+    if (dense == 0) return set_error(W4A16_ERR_WEIGHTS, "this engine has no dense FFN layer to quantize");
+    if (covered != dense)
+        return set_error(W4A16_ERR_WEIGHTS, "the sidecar covers %d of %d dense layers", covered, dense);
+
+    const long long H = c.hidden, I = c.intermediate, r = c.tp_rank;
+    const long long li = eng->local_inter;
+    std::vector<LayerOperands> staged(c.num_layers);
+    for (int l = 0; l < c.num_layers; ++l) {
+        if (!eng->dense[l]) continue;
+        const PairEntry &pair = m.pairs[m.find_pair("mlpGateUp", l)];
+        const Entry &down = m.entries[m.find_entry(l, "mlpDown")];
+        if (pair.n != 2 * I || pair.k != H)
+            return set_error(W4A16_ERR_WEIGHTS, "layer %d's mlpGateUp pair is [%lld, %lld], the checkpoint's gate+up is "
+                             "[%lld, %lld]", l, pair.n, pair.k, 2 * I, H);
+        if (down.n != H || down.k != I)
+            return set_error(W4A16_ERR_WEIGHTS, "layer %d's mlpDown is [%lld, %lld], the checkpoint's is [%lld, %lld]",
+                             l, down.n, down.k, H, I);
+        if (pair.group != down.group)
+            return set_error(W4A16_ERR_WEIGHTS, "layer %d's gate/up and down disagree on the group width", l);
+        /* this rank's extents: gate/up rows [r*li, (r+1)*li) of each half, down columns the same */
+        const long long col_off = r * li;
+        if (col_off % down.group != 0 || li % down.group != 0)
+            return set_error(W4A16_ERR_WEIGHTS, "layer %d's rank %lld splits K at a non-group boundary (column %lld), "
+                             "which cannot retain the global scales", l, r, col_off);
+        std::vector<uint8_t> gp, gs, dp, ds;
+        if (artifact_read(root, pair.packed, "u8", &gp) || artifact_read(root, pair.scales, "bf16", &gs) ||
+            artifact_read(root, down.packed, "u8", &dp) || artifact_read(root, down.scales, "bf16", &ds))
+            return W4A16_ERR_WEIGHTS;
+        const long long G = H / W4A16_GROUP, Gd = I / W4A16_GROUP, lGd = li / W4A16_GROUP;
+        std::vector<uint8_t> sgp((size_t)(2 * li * H / 2)), sgs((size_t)(2 * li * G * 2));
+        slice_rows(sgp.data(), gp.data(), H / 2, col_off, li, 0, H / 2);
+        slice_rows(sgp.data() + li * H / 2, gp.data(), H / 2, I + col_off, li, 0, H / 2);
+        slice_rows(sgs.data(), gs.data(), G * 2, col_off, li, 0, G * 2);
+        slice_rows(sgs.data() + li * G * 2, gs.data(), G * 2, I + col_off, li, 0, G * 2);
+        std::vector<uint8_t> sdp((size_t)(H * li / 2)), sds((size_t)(H * lGd * 2));
+        slice_rows(sdp.data(), dp.data(), I / 2, 0, H, col_off / 2, li / 2);
+        slice_rows(sds.data(), ds.data(), Gd * 2, 0, H, col_off / W4A16_GROUP * 2, lGd * 2);
+        LayerOperands &op = staged[l];
+        if ((st = upload_tiled(sgp, sgs, 2 * li, H, 1, &op.gu_packed, &op.gu_scales)) ||
+            (st = upload_tiled(sdp, sds, H, li, 0, &op.dn_packed, &op.dn_scales)))
+            return set_error(W4A16_ERR_WEIGHTS, "%s", join_error("upload: ").c_str());
+        op.loaded = true;
+    }
+    DevBuf ws;
+    if (ws.alloc((size_t)c.max_tokens * (size_t)li * 2)) return W4A16_ERR_WEIGHTS;
+    /* commit: only now does the handle see the new operands */
+    eng->layers.swap(staged);
+    eng->act_ws = std::move(ws);
+    eng->quantized_layers = dense;
+    return W4A16_OK;
+}
+
+}  // namespace
+
+extern "C" const char *engine_last_error(void) { return w4a16_last_error(); }
+
+extern "C" EngineHandle *w4a16_engine_create(const W4A16EngineConfig *cfg) {
+    if (!cfg) {
+        set_error(W4A16_ERR_CONFIG, "engine_create: null config");
+        return nullptr;
+    }
+    const W4A16EngineConfig &c = *cfg;
+    if (c.num_layers <= 0 || c.hidden <= 0 || c.intermediate <= 0 || c.tp_size <= 0 ||
+        c.tp_rank < 0 || c.tp_rank >= c.tp_size || c.max_tokens <= 0 || c.ep_size <= 0) {
+        set_error(W4A16_ERR_CONFIG, "engine_create: bad configuration");
+        return nullptr;
+    }
+    if (c.intermediate % c.tp_size != 0) {
+        set_error(W4A16_ERR_CONFIG, "engine_create: intermediate %d does not split over tp=%d",
+                  c.intermediate, c.tp_size);
+        return nullptr;
+    }
+    auto eng = std::make_unique<EngineHandle>();
+    eng->cfg = c;
+    eng->dense.assign((size_t)c.num_layers, 1);
+    if (c.layer_is_dense)
+        for (int l = 0; l < c.num_layers; ++l) eng->dense[l] = c.layer_is_dense[l] ? 1 : 0;
+    eng->local_inter = c.intermediate / c.tp_size;
+    eng->layers.resize((size_t)c.num_layers);
+    return eng.release();
+}
+
+extern "C" void w4a16_engine_destroy(EngineHandle *eng) { delete eng; }
+
+extern "C" int engine_load_quantized_ffn(EngineHandle *eng, const char *manifest_dir) {
+    if (!eng || !manifest_dir) return set_error(W4A16_ERR_CONFIG, "engine_load_quantized_ffn: null argument");
+    try {
+        const int st = load_impl(eng, manifest_dir);
+        if (st) {
+            const std::string why = w4a16_last_error();
+            return set_error(W4A16_ERR_WEIGHTS, "engine_load_quantized_ffn: %s", why.c_str());
+        }
+        return W4A16_OK;
+    } catch (const std::exception &e) {
+        return set_error(W4A16_ERR_WEIGHTS, "engine_load_quantized_ffn: %s", e.what());
+    }
+}
+
+extern "C" int engine_quantized_ffn_layers(const EngineHandle *eng) {
+    return eng ? eng->quantized_layers : 0;
+}
+
+extern "C" int engine_ffn_operands(const EngineHandle *eng, int layer, W4A16FfnOperands *out) {
+    if (!eng || !out) return set_error(W4A16_ERR_CONFIG, "engine_ffn_operands: null argument");
+    if (layer < 0 || layer >= eng->cfg.num_layers || !eng->layers[layer].loaded)
+        return set_error(W4A16_ERR_STATE, "engine_ffn_operands: layer %d has no INT4 operands", layer);
+    const LayerOperands &op = eng->layers[layer];
+    out->gate_up_packed = static_cast<const uint8_t *>(op.gu_packed.ptr);
+    out->gate_up_scales = static_cast<const uint16_t *>(op.gu_scales.ptr);
+    out->down_packed = static_cast<const uint8_t *>(op.dn_packed.ptr);
+    out->down_scales = static_cast<const uint16_t *>(op.dn_scales.ptr);
+    out->hidden = eng->cfg.hidden;
+    out->intermediate = eng->local_inter;
+    out->group = W4A16_GROUP;
+    return W4A16_OK;
+}
+
+static int ffn_forward(EngineHandle *eng, int layer, const uint16_t *normed, void *out,
+                       bool partial, int tokens, void *stream) {
+    W4A16FfnOperands op;
+    int st = engine_ffn_operands(eng, layer, &op);
+    if (st) return st;
+    if (tokens < 0 || tokens > eng->cfg.max_tokens)
+        return set_error(W4A16_ERR_CONFIG, "engine_ffn_forward: %d tokens, this engine holds workspace for %d",
+                         tokens, eng->cfg.max_tokens);
+    uint16_t *act = static_cast<uint16_t *>(eng->act_ws.ptr);
+    return partial ? mlp_int4_partial_f32(normed, op.gate_up_packed, op.gate_up_scales, op.down_packed,
+                                          op.down_scales, static_cast<float *>(out), act, tokens,
+                                          op.hidden, op.intermediate, stream)
+                   : mlp_int4_bf16(normed, op.gate_up_packed, op.gate_up_scales, op.down_packed,
+                                   op.down_scales, static_cast<uint16_t *>(out), act, tokens,
+                                   op.hidden, op.intermediate, stream);
+}
+
+extern "C" int engine_ffn_forward(EngineHandle *eng, int layer, const uint16_t *normed,
+                                  uint16_t *out, int tokens, void *stream) {
+    return ffn_forward(eng, layer, normed, out, false, tokens, stream);
+}
+
+extern "C" int engine_ffn_forward_partial_f32(EngineHandle *eng, int layer,
+                                              const uint16_t *normed, float *out, int tokens,
+                                              void *stream) {
+    return ffn_forward(eng, layer, normed, out, true, tokens, stream);
+}

@@ -63,6 +63,18 @@ _SIGNATURES = {
     "gate_up_silu_int4_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mlp_int4_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mlp_int4_partial_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "w4a16_manifest_check": (_i, [ctypes.c_char_p, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
+    "w4a16_artifact_verify": (_i, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _ll,
+                                   ctypes.c_char_p, ctypes.c_char_p]),
+    "w4a16_sha256_hex": (_i, [_vp, ctypes.c_size_t, ctypes.c_char_p]),
+    "w4a16_engine_create": (_vp, [_vp]),
+    "w4a16_engine_destroy": (None, [_vp]),
+    "engine_load_quantized_ffn": (_i, [_vp, ctypes.c_char_p]),
+    "engine_last_error": (ctypes.c_char_p, []),
+    "engine_quantized_ffn_layers": (_i, [_vp]),
+    "engine_ffn_operands": (_i, [_vp, _i, _vp]),
+    "engine_ffn_forward": (_i, [_vp, _i, _vp, _vp, _i, _vp]),
+    "engine_ffn_forward_partial_f32": (_i, [_vp, _i, _vp, _vp, _i, _vp]),
     "test_gemm_int4": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i]),
     "test_silu_mul_packed": (_i, [_vp, _vp, _i, _i]),
 }
@@ -295,3 +307,96 @@ def mlp_int4(x, gu, dn, out=None, act_ws=None, partial_f32=False, stream=None):
               dn.scales.data_ptr(), out.data_ptr(), act_ws.data_ptr(), m, h, inter,
               _stream(stream)), "mlp_int4")
     return out
+
+
+# ----------------------------------------------------------------------------------------------
+# Sidecar and the operand store (engine_load_quantized_ffn)
+# ----------------------------------------------------------------------------------------------
+
+MANIFEST_OK, MANIFEST_ERR_ARG, MANIFEST_ERR_SYNTAX, MANIFEST_ERR_FORMAT = 0, 1, 2, 3
+MANIFEST_ERR_SHAPE, MANIFEST_ERR_IO, MANIFEST_ERR_HASH = 4, 5, 6
+
+
+def manifest_check(text):
+    """Status of parsing and validating a sidecar document (0 ok; 1-6 as the reference reader)."""
+    e, p = _i(0), _i(0)
+    st = lib.w4a16_manifest_check(text.encode() if isinstance(text, str) else text,
+                                  ctypes.byref(e), ctypes.byref(p))
+    return st, e.value, p.value
+
+
+def artifact_verify(root, file, dtype, nbytes, sha256_hex, want_dtype):
+    return lib.w4a16_artifact_verify(root.encode(), file.encode(), dtype.encode(), nbytes,
+                                     sha256_hex.encode(), want_dtype.encode() if want_dtype else None)
+
+
+def sha256_hex(data):
+    buf = ctypes.create_string_buffer(65)
+    arr = np.frombuffer(data, dtype=np.uint8) if len(data) else np.zeros(1, np.uint8)
+    _check(lib.w4a16_sha256_hex(arr.ctypes.data, len(data), buf), "sha256")
+    return buf.value.decode()
+
+
+class _EngineConfig(ctypes.Structure):
+    _fields_ = [("num_layers", _i), ("layer_is_dense", ctypes.POINTER(ctypes.c_ubyte)),
+                ("hidden", _i), ("intermediate", _i), ("tp_size", _i), ("tp_rank", _i),
+                ("ep_size", _i), ("max_tokens", _i)]
+
+
+class FfnOperands(ctypes.Structure):
+    _fields_ = [("gate_up_packed", _vp), ("gate_up_scales", _vp), ("down_packed", _vp),
+                ("down_scales", _vp), ("hidden", _i), ("intermediate", _i), ("group", _i)]
+
+
+class Engine:
+    """The INT4 FFN operand store of one GPU (EngineHandle)."""
+
+    def __init__(self, num_layers, hidden, intermediate, tp_size=1, tp_rank=0, ep_size=1,
+                 max_tokens=16, dense=None):
+        flags = None
+        if dense is not None:
+            self._dense = (ctypes.c_ubyte * num_layers)(*[1 if d else 0 for d in dense])
+            flags = ctypes.cast(self._dense, ctypes.POINTER(ctypes.c_ubyte))
+        cfg = _EngineConfig(num_layers, flags, hidden, intermediate, tp_size, tp_rank, ep_size,
+                            max_tokens)
+        self.handle = lib.w4a16_engine_create(ctypes.byref(cfg))
+        if not self.handle:
+            raise W4A16Error(W4A16_ERR_CONFIG, f"engine_create: {last_error()}")
+        self.hidden, self.intermediate, self.tp_size = hidden, intermediate, tp_size
+
+    def close(self):
+        if self.handle:
+            lib.w4a16_engine_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+    def load_quantized_ffn(self, manifest_dir):
+        """engine_load_quantized_ffn: returns the status (0 ok); raises nothing."""
+        return lib.engine_load_quantized_ffn(self.handle, manifest_dir.encode())
+
+    @staticmethod
+    def last_error():
+        return lib.engine_last_error().decode(errors="replace")
+
+    @property
+    def quantized_layers(self):
+        return lib.engine_quantized_ffn_layers(self.handle)
+
+    def operands(self, layer):
+        op = FfnOperands()
+        _check(lib.engine_ffn_operands(self.handle, layer, ctypes.byref(op)), "engine_ffn_operands")
+        return op
+
+    def forward(self, layer, normed, out=None, partial_f32=False, stream=None):
+        import torch
+
+        m = normed.shape[0]
+        if out is None:
+            out = torch.empty((m, self.hidden), dtype=torch.float32 if partial_f32 else normed.dtype,
+                              device=normed.device)
+        fn = lib.engine_ffn_forward_partial_f32 if partial_f32 else lib.engine_ffn_forward
+        _check(fn(self.handle, layer, normed.data_ptr(), out.data_ptr(), m, _stream(stream)),
+               "engine_ffn_forward")
+        return out

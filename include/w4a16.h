@@ -133,6 +133,87 @@ int mlp_int4_partial_f32(const uint16_t *normed, const uint8_t *gu_packed,
                          int hidden, int intermediate, void *stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Sidecar and artifacts (host). Status values are the reference reader's QuantManifestStatus
+ * (reference csrc/include/quant_manifest.h:55-63): 0 ok, 1 arg, 2 syntax, 3 format, 4 shape,
+ * 5 io, 6 hash; the reason is in w4a16_last_error().
+ * ------------------------------------------------------------------------------------- */
+
+/* Parse and validate a weights.manifest.json document (no file access). Replaces
+ * quant_manifest_parse (reference csrc/quant_manifest.c:895-1063). */
+int w4a16_manifest_check(const char *json, int *entries, int *pairs);
+
+/* Read root/file, requiring `bytes`, the dtype and the SHA-256 the manifest recorded. Replaces
+ * quant_artifact_read (reference csrc/quant_manifest.c:1085-1139). */
+int w4a16_artifact_verify(const char *root, const char *file, const char *dtype, long long bytes,
+                          const char *sha256_hex, const char *want_dtype);
+
+/* Lowercase hex SHA-256 of a buffer into out_hex65 (64 digits + NUL). Replaces sha256_hex
+ * (reference csrc/include/sha256.h:41). */
+int w4a16_sha256_hex(const void *data, size_t len, char *out_hex65);
+
+/* ---------------------------------------------------------------------------------------
+ * The INT4 FFN operand store (load and decode dispatch).
+ * ------------------------------------------------------------------------------------- */
+
+/* The store's handle. It carries the part of the reference engine that the INT4 path reads:
+ * the descriptor's dense layers and FFN sizes, the tensor-parallel degree and this handle's
+ * rank (one handle per GPU), and the device operands it loads. */
+typedef struct EngineHandle EngineHandle;
+
+typedef struct W4A16EngineConfig {
+    int num_layers;
+    const unsigned char *layer_is_dense; /* num_layers flags; NULL = every layer dense */
+    int hidden;                          /* hidden_size */
+    int intermediate;                    /* the checkpoint's full intermediate_size */
+    int tp_size;                         /* replicated tensor parallelism degree */
+    int tp_rank;                         /* this handle's rank */
+    int ep_size;                         /* expert parallelism (> 1 is refused at load) */
+    int max_tokens;                      /* largest M engine_ffn_forward accepts */
+} W4A16EngineConfig;
+
+/* Device operands of one layer, in tile order (the reference's LayerWeights::{gate_up_i4,
+ * gate_up_i4_scales, down_i4, down_i4_scales, i4_group}, reference csrc/include/layers.h:158-165). */
+typedef struct W4A16FfnOperands {
+    const uint8_t *gate_up_packed;
+    const uint16_t *gate_up_scales;
+    const uint8_t *down_packed;
+    const uint16_t *down_scales;
+    int hidden;
+    int intermediate; /* this rank's share */
+    int group;
+} W4A16FfnOperands;
+
+/* No reference counterpart: the reference engine_create (csrc/include/engine.h:69-72) builds
+ * these fields from its descriptor. NULL on a bad configuration (w4a16_last_error()). */
+EngineHandle *w4a16_engine_create(const W4A16EngineConfig *cfg);
+void w4a16_engine_destroy(EngineHandle *engine);
+
+/* Load the INT4 operands of every dense layer from manifest_dir (weights.manifest.json + the
+ * artifacts it names): validated, SHA-256 checked, sliced to this rank with the global scales,
+ * uploaded and re-laid on the device; all-or-nothing. W4A16_OK, W4A16_ERR_CONFIG for a null
+ * argument, otherwise W4A16_ERR_WEIGHTS with the reason in engine_last_error().
+ * Same signature and semantics as reference csrc/include/engine.h:98 (csrc/engine.cu:2207-2428). */
+int engine_load_quantized_ffn(EngineHandle *engine, const char *manifest_dir);
+
+/* Reason of the calling thread's last failure (reference csrc/include/engine.h, engine_last_error). */
+const char *engine_last_error(void);
+
+/* Number of dense layers holding INT4 operands (the reference's quantized_ffn_layers). */
+int engine_quantized_ffn_layers(const EngineHandle *engine);
+
+/* The layer's device operands (W4A16_ERR_STATE if the layer has none). */
+int engine_ffn_operands(const EngineHandle *engine, int layer, W4A16FfnOperands *out);
+
+/* The INT4 branch of forward_mlp_prepared for one layer (reference csrc/kernels/layers.cu:126-145
+ * and 163-169): normed [tokens, hidden] BF16 -> out [tokens, hidden] BF16 on `stream`, using the
+ * handle's workspace. Under tensor parallelism the _partial_f32 form returns this rank's FP32
+ * down-projection partial, to be summed across ranks before rounding. */
+int engine_ffn_forward(EngineHandle *engine, int layer, const uint16_t *normed, uint16_t *out,
+                       int tokens, void *stream);
+int engine_ffn_forward_partial_f32(EngineHandle *engine, int layer, const uint16_t *normed,
+                                   float *out, int tokens, void *stream);
+
+/* ---------------------------------------------------------------------------------------
  * Test bridges (host pointers, artifact layout; synchronous).
  * ------------------------------------------------------------------------------------- */
 

@@ -1,0 +1,119 @@
+"""The loaded path on cuda:0: convert -> engine_load_quantized_ffn -> engine_ffn_forward.
+
+* Every dense layer's operands, dequantized from tile order on the device, equal the oracle's
+  dequantization of the artifact bytes bit for bit (tp=1, and each rank's slice at tp=2 with the
+  global scales: reference csrc/engine.cu:2308-2395).
+* engine_ffn_forward of each layer matches the oracle FFN (rel-L2 <= 1e-3, <= 2 BF16 ULP at
+  the rms/16 floor, see test_gpu_parity.test_ffn_parity).
+* At tp=2 the two ranks' FP32 partials sum to the full FFN within the same bar, and the sum is
+  what a BF16 all-reduce would see.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import convert
+import w4a16
+from conftest import assert_parity
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+H, I, LAYERS = 2560, 9728, 2
+
+
+@pytest.fixture(scope="module")
+def model(tmp_path_factory):
+    out = str(tmp_path_factory.mktemp("int4_model"))
+    layers = {}
+    for layer in range(LAYERS):
+        layers[layer] = {
+            "mlpGate": oracle.synth_weight(I, H, 1000 + 3 * layer),
+            "mlpUp": oracle.synth_weight(I, H, 1001 + 3 * layer),
+            "mlpDown": oracle.synth_weight(H, I, 1002 + 3 * layer),
+        }
+    convert.write_sidecar(out, layers, "/tmp/synthetic-qwen3-4b-ffn")
+    arts = {}
+    for layer in range(LAYERS):
+        gp, gs = oracle.quantize(layers[layer]["mlpGate"])
+        up, us = oracle.quantize(layers[layer]["mlpUp"])
+        dp, ds = oracle.quantize(layers[layer]["mlpDown"])
+        arts[layer] = (np.concatenate([gp, up]), np.concatenate([gs, us]), dp, ds)
+    return out, arts
+
+
+def dequant_operand(ptr_p, ptr_s, n, k, pair, device):
+    import torch
+
+    out = torch.empty((n, k), dtype=torch.float32, device=device)
+    st = w4a16.lib.w4a16_dequant_tiled_device(n, k, int(pair), ptr_p, ptr_s, out.data_ptr(),
+                                              torch.cuda.current_stream().cuda_stream)
+    assert st == 0, w4a16.last_error()
+    return out.cpu().numpy()
+
+
+def test_load_and_forward_tp1(cuda, model):
+    import torch
+
+    out, arts = model
+    print("engine tp=1 load", flush=True)
+    eng = w4a16.Engine(LAYERS, H, I)
+    assert eng.load_quantized_ffn(out) == 0, eng.last_error()
+    assert eng.quantized_layers == LAYERS
+    x = oracle.synth_activation(1, H, 7)
+    xd = torch.from_numpy(x.view(np.int16)).to(cuda)
+    for layer in range(LAYERS):
+        gup, gus, dp, ds = arts[layer]
+        op = eng.operands(layer)
+        assert (op.hidden, op.intermediate, op.group) == (H, I, 128)
+        deq = dequant_operand(op.gate_up_packed, op.gate_up_scales, 2 * I, H, True, cuda)
+        assert np.array_equal(deq.view(np.uint32),
+                              oracle.dequantize_numpy(gup, gus, 2 * I, H).view(np.uint32))
+        deq = dequant_operand(op.down_packed, op.down_scales, H, I, False, cuda)
+        assert np.array_equal(deq.view(np.uint32),
+                              oracle.dequantize_numpy(dp, ds, H, I).view(np.uint32))
+        print(f"engine tp=1 forward layer {layer}", flush=True)
+        got = eng.forward(layer, xd).cpu().numpy().view(np.uint16)
+        ref, _, _ = oracle.ffn_bf16(x, gup, gus, dp, ds, H, I)
+        assert_parity(got, ref, f"engine layer {layer}", floor_div=16.0)
+    eng.close()
+
+
+def test_load_and_forward_tp2(cuda, model):
+    import torch
+
+    out, arts = model
+    li = I // 2
+    x = oracle.synth_activation(1, H, 7)
+    xd = torch.from_numpy(x.view(np.int16)).to(cuda)
+    partials = []
+    for rank in range(2):
+        print(f"engine tp=2 rank {rank} load", flush=True)
+        eng = w4a16.Engine(LAYERS, H, I, tp_size=2, tp_rank=rank)
+        assert eng.load_quantized_ffn(out) == 0, eng.last_error()
+        gup, gus, dp, ds = arts[0]
+        rows = np.r_[rank * li:(rank + 1) * li, I + rank * li:I + (rank + 1) * li]
+        sgp, sgs = gup[rows], gus[rows]
+        sdp = np.ascontiguousarray(dp[:, rank * li // 2:(rank + 1) * li // 2])
+        sds = np.ascontiguousarray(ds[:, rank * li // 128:(rank + 1) * li // 128])
+        op = eng.operands(0)
+        assert op.intermediate == li
+        deq = dequant_operand(op.gate_up_packed, op.gate_up_scales, 2 * li, H, True, cuda)
+        assert np.array_equal(deq.view(np.uint32),
+                              oracle.dequantize_numpy(sgp, sgs, 2 * li, H).view(np.uint32))
+        deq = dequant_operand(op.down_packed, op.down_scales, H, li, False, cuda)
+        assert np.array_equal(deq.view(np.uint32),
+                              oracle.dequantize_numpy(sdp, sds, H, li).view(np.uint32))
+        print(f"engine tp=2 rank {rank} forward", flush=True)
+        part = eng.forward(0, xd, partial_f32=True).cpu().numpy()
+        want = oracle.ffn_partial_f32(x, sgp, sgs, sdp, sds, H, li)
+        rel = np.linalg.norm(part.astype(np.float64) - want) / np.linalg.norm(want)
+        assert rel <= 1e-3, rel
+        partials.append(part)
+        eng.close()
+    total = oracle.bf16_bits((partials[0].astype(np.float64) + partials[1]).astype(np.float32))
+    ref, _, _ = oracle.ffn_bf16(x, *arts[0], H, I)
+    assert_parity(total, ref, "tp=2 partial sum vs full FFN", floor_div=16.0)
