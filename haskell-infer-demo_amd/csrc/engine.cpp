@@ -239,6 +239,10 @@ extern "C" int engine_load_quantized_ffn(EngineHandle *eng, const char *manifest
     }
 }
 
+extern "C" int w4a16_load_quantized_ffn(EngineHandle *eng, const char *manifest_dir) {
+    return engine_load_quantized_ffn(eng, manifest_dir);
+}
+
 extern "C" int engine_quantized_ffn_layers(const EngineHandle *eng) {
     return eng ? eng->quantized_layers : 0;
 }

@@ -70,6 +70,7 @@ _SIGNATURES = {
     "w4a16_engine_create": (_vp, [_vp]),
     "w4a16_engine_destroy": (None, [_vp]),
     "engine_load_quantized_ffn": (_i, [_vp, ctypes.c_char_p]),
+    "w4a16_load_quantized_ffn": (_i, [_vp, ctypes.c_char_p]),
     "engine_last_error": (ctypes.c_char_p, []),
     "engine_quantized_ffn_layers": (_i, [_vp]),
     "engine_ffn_operands": (_i, [_vp, _i, _vp]),

@@ -194,6 +194,9 @@ void w4a16_engine_destroy(EngineHandle *engine);
  * argument, otherwise W4A16_ERR_WEIGHTS with the reason in engine_last_error().
  * Same signature and semantics as reference csrc/include/engine.h:98 (csrc/engine.cu:2207-2428). */
 int engine_load_quantized_ffn(EngineHandle *engine, const char *manifest_dir);
+/* The same function under a prefixed name, for an engine that defines the public name itself
+ * and calls this loader per rank from inside it. */
+int w4a16_load_quantized_ffn(EngineHandle *engine, const char *manifest_dir);
 
 /* Reason of the calling thread's last failure (reference csrc/include/engine.h, engine_last_error). */
 const char *engine_last_error(void);
