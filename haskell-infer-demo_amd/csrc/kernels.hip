@@ -246,7 +246,7 @@ __device__ __forceinline__ bf16x8_t unpack8(uint32_t word) {
     return __builtin_bit_cast(bf16x8_t, v);
 }
 
-template <int OUT, int XPRE>
+template <int OUT, int XPRE, int MI>
 __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
     const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, int S, int GS,
@@ -293,8 +293,11 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
         sbits[i] = buf_load_u16(sr, ok ? (unit * 8 + r) * 2 : kOob);
     }
 
-    /* 3. stage the activation (row-major [M][ng*128] BF16) and the group sums X[m][g] */
-    float *xsum = reinterpret_cast<float *>(smem4 + chunks);
+    /* 3. stage the activation (row-major [M][ng*128] BF16, then one zero row that the lanes of
+     * rows >= M read as their A operand) and the group sums X[m][g] */
+    uint4 *zero_row = smem4 + chunks;
+    for (int i = tid; i < cpr; i += kMfmaWaves * 64) zero_row[i] = make_uint4(0, 0, 0, 0);
+    float *xsum = reinterpret_cast<float *>(smem4 + chunks + cpr);
     auto stage = [&](int i, uint4 v) {
         if (i < chunks) smem4[i] = v;
         const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
@@ -319,29 +322,38 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
     __syncthreads();
     if (tp >= NT) return;
 
-    /* 4. four MFMAs per group, then scale and offset correction into acc[i] (row 4q + i) */
-    const int arow = min(n, M - 1);
-    const bool a_live = n < M;
+    /* 4. four MFMAs per group, then scale and offset correction into acc[i] (row 4q + i; only
+     * the MI first D registers can hold rows < M when M <= 4). Two groups are processed
+     * together so their MFMA chains interleave. */
+    const uint4 *arow_base = smem4 + (n < M ? n * cpr : chunks) + q;
     f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto group_mfma = [&](int gl) {
+        const uint32_t words[4] = {buf[gl].x, buf[gl].y, buf[gl].z, buf[gl].w};
+        const uint4 *xa = arow_base + gl * 16;
+        f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int gl = 0; gl < kGMax; ++gl) {
-        if (gl < ng) { /* block-uniform */
-            const uint32_t words[4] = {buf[gl].x, buf[gl].y, buf[gl].z, buf[gl].w};
-            const uint4 *xa = smem4 + arow * cpr + gl * 16 + q;
-            f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s = 0; s < 4; ++s)
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[4 * s]),
+                                                        unpack8(words[s]), d, 0, 0, 0);
+        return d;
+    };
+    auto group_fold = [&](int gl, const f32x4_t &d) {
+        const float sc = bf16_widen(sbits[gl]);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                uint4 av = xa[4 * s];
-                if (!a_live) av = make_uint4(0, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
-                                                            unpack8(words[s]), d, 0, 0, 0);
-            }
-            const float sc = bf16_widen(sbits[gl]);
+        for (int i = 0; i < MI; ++i) {
+            const int m = min(4 * q + i, M - 1);
+            acc[i] = fmaf(sc, fmaf(32.0f, d[i], -24.0f * xsum[m * ng + gl]), acc[i]);
+        }
+    };
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = min(4 * q + i, M - 1);
-                acc[i] = fmaf(sc, fmaf(32.0f, d[i], -24.0f * xsum[m * ng + gl]), acc[i]);
-            }
+    for (int gl = 0; gl < kGMax; gl += 2) {
+        if (gl + 1 < ng) { /* block-uniform */
+            const f32x4_t d0 = group_mfma(gl);
+            const f32x4_t d1 = group_mfma(gl + 1);
+            group_fold(gl, d0);
+            group_fold(gl + 1, d1);
+        } else if (gl < ng) {
+            group_fold(gl, group_mfma(gl));
         }
     }
 
@@ -363,15 +375,25 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
                                           __HIP_MEMORY_SCOPE_AGENT);
         prev = __shfl(prev, 0);
         if (prev != (unsigned)(S - 1)) return;
+        /* the S partials are loaded in batches of 8 with every load issued before any is
+         * summed (each is a round trip to the coherence point), then summed in split order */
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = 0.0f;
-        for (int k2 = 0; k2 < S; ++k2) {
-            const float *src = partial + ((size_t)k2 * NT + tp) * 16 * M;
+        for (int k0 = 0; k0 < S; k0 += 8) {
+            float v[8][MI];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (4 * q + i < M)
-                    acc[i] += __hip_atomic_load(src + (4 * q + i) * 16 + n, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
+            for (int j = 0; j < 8; ++j) {
+                const float *src = partial + ((size_t)min(k0 + j, S - 1) * NT + tp) * 16 * M;
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+                    v[j][i] = __hip_atomic_load(src + min(4 * q + i, M - 1) * 16 + n,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+                    if (k0 + j < S) acc[i] += v[j][i];
         }
         if (lane == 0)
             __hip_atomic_store(&counters[tp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -589,11 +611,13 @@ struct MfmaPlan {
 
 /* K split: at most kGMax groups per wave, activation range within 32 KiB of LDS, and enough
  * blocks that the waves cover the chip several times over. */
+int g_mfma_gmax = kGMax; /* groups per wave cap (tuning knob, <= kGMax) */
+
 MfmaPlan plan_mfma(int M, int N, int K) {
     MfmaPlan p{};
     const int G = K / 128;
     const int NT = (N / 8 + 1) / 2;
-    const int gmax = std::max(1, std::min(kGMax, 128 / M));
+    const int gmax = std::max(1, std::min(g_mfma_gmax, 128 / M));
     int S = (G + gmax - 1) / gmax;
     const int nblk = (NT + kMfmaWaves - 1) / kMfmaWaves;
     while ((long long)nblk * kMfmaWaves * S < 1024 && (G + S) / (S + 1) >= 4) ++S;
@@ -603,7 +627,7 @@ MfmaPlan plan_mfma(int M, int N, int K) {
     const int pre = (chunks + kMfmaWaves * 64 - 1) / (kMfmaWaves * 64);
     p.xpre = pre <= 1 ? 1 : pre <= 2 ? 2 : pre <= 4 ? 4 : 8;
     p.grid = nblk * p.S;
-    p.smem = (size_t)chunks * 16 + (size_t)M * p.GS * 4;
+    p.smem = (size_t)(chunks + p.GS * 16) * 16 + (size_t)M * p.GS * 4;
     p.partial_bytes = p.S > 1 ? (size_t)p.S * NT * 16 * M * 4 : 0;
     p.ncounters = p.S > 1 ? (size_t)NT : 0;
     return p;
@@ -613,8 +637,15 @@ template <int OUT, int XPRE>
 int launch_mfma_x(const MfmaPlan &p, const uint16_t *x, int M, const uint8_t *w,
                   const uint16_t *s, void *out, int N, int K, float *partial, unsigned *counters,
                   hipStream_t stream) {
-    hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE>), dim3(p.grid), dim3(kMfmaWaves * 64), p.smem,
-                       stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters);
+    if (M == 1)
+        hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE, 1>), dim3(p.grid), dim3(kMfmaWaves * 64),
+                           p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters);
+    else if (M == 2)
+        hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE, 2>), dim3(p.grid), dim3(kMfmaWaves * 64),
+                           p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters);
+    else
+        hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE, 4>), dim3(p.grid), dim3(kMfmaWaves * 64),
+                           p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters);
     return hip_status(hipGetLastError(), "mfma gemm launch");
 }
 
