@@ -75,7 +75,7 @@ struct EngineHandle {
     std::vector<unsigned char> dense;
     int local_inter = 0; /* intermediate columns this rank holds */
     std::vector<LayerOperands> layers;
-    DevBuf act_ws;       /* [max_tokens, local_inter] BF16 */
+    DevBuf act_ws;       /* [max_tokens, hidden + local_inter] BF16 (normed, then act) */
     int quantized_layers = 0;
 };
 
@@ -185,7 +185,7 @@ int load_impl(EngineHandle *eng, const std::string &root) {
         op.loaded = true;
     }
     DevBuf ws;
-    if (ws.alloc((size_t)c.max_tokens * (size_t)li * 2)) return W4A16_ERR_WEIGHTS;
+    if (ws.alloc((size_t)c.max_tokens * (size_t)(H + li) * 2)) return W4A16_ERR_WEIGHTS;
     /* commit: only now does the handle see the new operands */
     eng->layers.swap(staged);
     eng->act_ws = std::move(ws);
@@ -288,4 +288,40 @@ extern "C" int engine_ffn_forward_partial_f32(EngineHandle *eng, int layer,
                                               const uint16_t *normed, float *out, int tokens,
                                               void *stream) {
     return ffn_forward(eng, layer, normed, out, true, tokens, stream);
+}
+
+static int ffn_forward_norm(EngineHandle *eng, int layer, const uint16_t *residual,
+                            const uint16_t *norm_w, int norm_style, float eps, void *out,
+                            bool partial, int tokens, void *stream) {
+    W4A16FfnOperands op;
+    int st = engine_ffn_operands(eng, layer, &op);
+    if (st) return st;
+    if (tokens < 0 || tokens > eng->cfg.max_tokens)
+        return set_error(W4A16_ERR_CONFIG, "engine_ffn_forward_norm: %d tokens, this engine holds workspace for %d",
+                         tokens, eng->cfg.max_tokens);
+    uint16_t *ws = static_cast<uint16_t *>(eng->act_ws.ptr);
+    return partial ? mlp_int4_norm_partial_f32(residual, norm_w, norm_style, eps, op.gate_up_packed,
+                                               op.gate_up_scales, op.down_packed, op.down_scales,
+                                               static_cast<float *>(out), ws, tokens, op.hidden,
+                                               op.intermediate, stream)
+                   : mlp_int4_norm_bf16(residual, norm_w, norm_style, eps, op.gate_up_packed,
+                                        op.gate_up_scales, op.down_packed, op.down_scales,
+                                        static_cast<uint16_t *>(out), ws, tokens, op.hidden,
+                                        op.intermediate, stream);
+}
+
+extern "C" int engine_ffn_forward_norm(EngineHandle *eng, int layer, const uint16_t *residual,
+                                       const uint16_t *norm_w, int norm_style, float eps,
+                                       uint16_t *out, int tokens, void *stream) {
+    return ffn_forward_norm(eng, layer, residual, norm_w, norm_style, eps, out, false, tokens,
+                            stream);
+}
+
+extern "C" int engine_ffn_forward_norm_partial_f32(EngineHandle *eng, int layer,
+                                                   const uint16_t *residual,
+                                                   const uint16_t *norm_w, int norm_style,
+                                                   float eps, float *out, int tokens,
+                                                   void *stream) {
+    return ffn_forward_norm(eng, layer, residual, norm_w, norm_style, eps, out, true, tokens,
+                            stream);
 }

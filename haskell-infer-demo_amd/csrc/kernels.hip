@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <mutex>
 
@@ -102,10 +103,11 @@ constexpr uint32_t kOob = 0x80000000u; /* an offset no buffer here reaches: read
  * wait covers the activation and the weights stream while it is staged into LDS.
  * PAIR: a tile is 4 gate + 4 up rows and yields four BF16(silu(BF16 gate) x BF16 up) values;
  * otherwise eight BF16 outputs (or FP32 if OUT_F32). */
-template <bool PAIR, bool OUT_F32, int TB, int SK>
+template <bool PAIR, bool OUT_F32, int TB, int SK, bool NORM>
 __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ wt,
-    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K) {
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K,
+    const uint16_t *__restrict__ norm_w, float norm_bias, float eps) {
     constexpr int W = TB * SK;
     /* the largest K this configuration is launched for: SK * kMaxLoads group pairs */
     constexpr int kMaxK = (256 * kMaxLoads * SK < kMaxGemvK) ? 256 * kMaxLoads * SK : kMaxGemvK;
@@ -137,6 +139,15 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
         const int i = it * W * 64 + tid;
         xv[it] = buf_load16(xr, i < xchunks ? (uint32_t)i * 16 : kOob);
     }
+    uint4 nv[NORM ? kXIters : 1];
+    if (NORM) {
+        const __amdgpu_buffer_rsrc_t nr = make_rsrc(norm_w, (uint32_t)K * 2);
+#pragma unroll
+        for (int it = 0; it < kXIters; ++it) {
+            const int i = it * W * 64 + tid;
+            nv[it] = buf_load16(nr, i < xchunks ? (uint32_t)i * 16 : kOob);
+        }
+    }
 
     /* 2. every weight piece and scale of this wave */
     const bool tile_ok = tile < tiles;
@@ -154,6 +165,46 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
         const bool ok = p < P && g < G;
         buf[i] = buf_load16(wr, ok ? (uint32_t)(g * 512 + piece * 16) : kOob);
         sbits[i] = buf_load_u16(sr, ok ? (uint32_t)(g * 16 + r * 2) : kOob);
+    }
+
+    /* 2b. NORM: the activation is the RMSNorm of x, formed here (every block sees all of x):
+     * BF16(x * rsqrt(sum x^2 / K + eps) * (norm_bias + w)), the FP32 order of the reference's
+     * norm (FlashInfer RMSNorm / GemmaRMSNorm behind csrc/kernels/flashinfer_norm.cu:22-76) */
+    if (NORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int it = 0; it < kXIters; ++it) {
+            const uint32_t w4[4] = {xv[it].x, xv[it].y, xv[it].z, xv[it].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float lo = bf16_widen((uint16_t)(w4[q] & 0xFFFFu));
+                const float hi = bf16_widen((uint16_t)(w4[q] >> 16));
+                ss = fmaf(lo, lo, ss);
+                ss = fmaf(hi, hi, ss);
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        float total = 0.0f;
+        for (int w = 0; w < W; ++w) total += red[w];
+        const float rms = 1.0f / sqrtf(total / (float)K + eps);
+#pragma unroll
+        for (int it = 0; it < kXIters; ++it) {
+            uint32_t w4[4] = {xv[it].x, xv[it].y, xv[it].z, xv[it].w};
+            const uint32_t n4[4] = {nv[it].x, nv[it].y, nv[it].z, nv[it].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float lo = bf16_widen((uint16_t)(w4[q] & 0xFFFFu)) * rms *
+                                 (norm_bias + bf16_widen((uint16_t)(n4[q] & 0xFFFFu)));
+                const float hi = bf16_widen((uint16_t)(w4[q] >> 16)) * rms *
+                                 (norm_bias + bf16_widen((uint16_t)(n4[q] >> 16)));
+                w4[q] = (uint32_t)bf16_rne(lo) | ((uint32_t)bf16_rne(hi) << 16);
+            }
+            xv[it] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+        __syncthreads(); /* red is reused by the split-K reduction */
     }
 
     /* 3. stage the activation and the per-(group, kb) sums of the codes' x values */
@@ -216,6 +267,118 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
             reinterpret_cast<uint16_t *>(out)[tile * 8 + lane] = bf16_rne(row_sum);
     }
 }
+
+/* GEMV with wave-local activation: as gemv_tiles_kernel, but each wave loads only the
+ * activation of its own group pairs (512 bytes a pair, 8 bytes a lane, issued with its weight
+ * loads) into a private LDS slice, and forms the per-(group, kb) sums with shuffles. No block
+ * barrier stands between a wave's loads and its dot products, so a wave starts as soon as its
+ * own data arrives; the only barrier is the final split-K reduction. Suits a long K (the down
+ * projection), where staging the whole activation per block costs a round trip before any
+ * compute can start. NP: group pairs per wave (SK * NP >= pairs). */
+template <bool PAIR, bool OUT_F32, int TB, int SK, int NP>
+__global__ __launch_bounds__(TB * SK * 64) void gemv_xwave_kernel(
+    const uint16_t *__restrict__ x, const uint8_t *__restrict__ wt,
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K) {
+    constexpr int W = TB * SK;
+    extern __shared__ uint4 smem4[];
+    const int G = K >> 7;
+    const int P = (G + 1) >> 1;
+    const int tiles = N >> 3;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = blockIdx.x * TB + wave / SK;
+    const int ks = wave % SK;
+    const int half = lane >> 5;
+    const int piece = lane & 31;
+    const int kb = piece >> 3;
+    const int r = piece & 7;
+    uint4 *xslice = smem4 + wave * NP * 32; /* pair i: 32 chunks of 16 bytes */
+    float *red = reinterpret_cast<float *>(smem4 + W * NP * 32);
+
+    /* 1. this wave's activation (pair p: values [256 p, 256 p + 256), lane l holds 4 l..4 l+3),
+     * then its weight pieces and scales */
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)K * 2);
+    uint2 xv[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const int p = ks + i * SK;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(
+            xr, p < P ? (int)(p * 512 + lane * 8) : (int)kOob, 0, 0);
+        xv[i] = __builtin_bit_cast(uint2, v);
+    }
+    const bool tile_ok = tile < tiles;
+    const size_t tile_bytes = (size_t)G * 512;
+    const __amdgpu_buffer_rsrc_t wr =
+        make_rsrc(wt + (size_t)(tile_ok ? tile : 0) * tile_bytes, tile_ok ? (uint32_t)tile_bytes : 0);
+    const __amdgpu_buffer_rsrc_t sr =
+        make_rsrc(st + (size_t)(tile_ok ? tile : 0) * G * 8, tile_ok ? (uint32_t)G * 16 : 0);
+    uint4 buf[NP];
+    uint16_t sbits[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const int p = ks + i * SK;
+        const int g = 2 * p + half;
+        const bool ok = p < P && g < G;
+        buf[i] = buf_load16(wr, ok ? (uint32_t)(g * 512 + piece * 16) : kOob);
+        sbits[i] = buf_load_u16(sr, ok ? (uint32_t)(g * 16 + r * 2) : kOob);
+    }
+
+    /* 2. per pair: stage into the wave's slice, sums per (group, kb), dot products */
+    float acc = 0.0f;
+    uint2 *xs2 = reinterpret_cast<uint2 *>(xslice);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        if (ks + i * SK < P) { /* wave-uniform */
+            xs2[i * 64 + lane] = xv[i];
+            /* lane l holds chunk c = l / 2 = 16 gl + 4 s + kb of the pair: add the chunk's two
+             * halves (xor 1) and its four s (xor 8, 16); lane 32 gl + 2 kb then holds (gl, kb) */
+            float s4 = bf16_widen((uint16_t)(xv[i].x & 0xFFFFu)) + bf16_widen((uint16_t)(xv[i].x >> 16)) +
+                       bf16_widen((uint16_t)(xv[i].y & 0xFFFFu)) + bf16_widen((uint16_t)(xv[i].y >> 16));
+            s4 += __shfl_xor(s4, 1);
+            s4 += __shfl_xor(s4, 8);
+            s4 += __shfl_xor(s4, 16);
+            const float xsum = __shfl(s4, 32 * half + 2 * kb);
+            const uint4 *xq = xslice + i * 32 + 16 * half + kb;
+            const uint4 xrow[4] = {xq[0], xq[4], xq[8], xq[12]};
+            acc = fmaf(piece_dot(buf[i], xrow, xsum), bf16_widen(sbits[i]), acc);
+        }
+    }
+
+    /* 3. lanes r, r+8, ..., r+56 hold row r's partials; then the SK waves of a tile */
+    acc += __shfl_xor(acc, 8);
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    float row_sum = acc;
+    if (SK > 1) {
+        if (lane < 8) red[wave * 8 + lane] = acc;
+        __syncthreads();
+        if (ks == 0 && lane < 8) {
+            row_sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < SK; ++w) row_sum += red[(wave + w) * 8 + lane];
+        }
+    }
+    if (ks != 0 || !tile_ok) return;
+    if (PAIR) {
+        const float upv = __shfl_down(row_sum, 4);
+        if (lane < 4) {
+            const float gate = bf16_widen(bf16_rne(row_sum));
+            const float up = bf16_widen(bf16_rne(upv));
+            reinterpret_cast<uint16_t *>(out)[tile * 4 + lane] = silu_mul_bf16(gate, up);
+        }
+    } else if (lane < 8) {
+        if (OUT_F32)
+            reinterpret_cast<float *>(out)[tile * 8 + lane] = row_sum;
+        else
+            reinterpret_cast<uint16_t *>(out)[tile * 8 + lane] = bf16_rne(row_sum);
+    }
+}
+
+size_t xwave_smem(int waves, int np) { return (size_t)waves * np * 512 + (size_t)waves * 32; }
+constexpr int kXwaveWaves = 16;
+
 
 /* ------------------------------------------------------------------------------------------
  * MFMA form (M = 1..16 activation rows): v_mfma_f32_16x16x32_bf16 with the activation as the A
@@ -428,6 +591,30 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
     }
 }
 
+/* RMSNorm of each row (one block a row): BF16(x * rsqrt(sum x^2 / cols + eps) * (bias + w)),
+ * FP32 arithmetic (reference csrc/kernels/flashinfer_norm.cu:22-76). */
+__global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t *__restrict__ out,
+                                                      const uint16_t *__restrict__ x,
+                                                      const uint16_t *__restrict__ w, int cols,
+                                                      float bias, float eps) {
+    __shared__ float red[4];
+    const uint16_t *xr = x + (size_t)blockIdx.x * cols;
+    uint16_t *orow = out + (size_t)blockIdx.x * cols;
+    float ss = 0.0f;
+    for (int c = threadIdx.x; c < cols; c += 256) {
+        const float v = bf16_widen(xr[c]);
+        ss = fmaf(v, v, ss);
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = red[0] + red[1] + red[2] + red[3];
+    const float rms = 1.0f / sqrtf(total / (float)cols + eps);
+    for (int c = threadIdx.x; c < cols; c += 256)
+        orow[c] = bf16_rne(bf16_widen(xr[c]) * rms * (bias + bf16_widen(w[c])));
+}
+
 __global__ void silu_mul_packed_kernel(uint16_t *__restrict__ out,
                                        const uint16_t *__restrict__ packed, int tokens,
                                        int inter) {
@@ -530,29 +717,71 @@ size_t gemv_smem(int K, int waves) {
     return (size_t)K * 2 + (size_t)(K / 128) * 16 + (size_t)waves * 32;
 }
 
+/* Optional RMSNorm prologue of a GEMV (gate/up only): weight, bias (1 Gemma, 0 plain), eps. */
+struct NormArgs {
+    const uint16_t *w = nullptr;
+    float bias = 0.0f, eps = 0.0f;
+};
+
 template <bool PAIR, bool OUT_F32, int TB, int SK>
 int launch_gemv_cfg(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N,
-                    int K, hipStream_t stream) {
+                    int K, hipStream_t stream, const NormArgs *norm = nullptr) {
     const int tiles = N / 8;
-    hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK>), dim3((tiles + TB - 1) / TB),
-                       dim3(TB * SK * 64), gemv_smem(K, TB * SK), stream, x, w, s, out, N, K);
+    if (norm)
+        hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK, true>),
+                           dim3((tiles + TB - 1) / TB), dim3(TB * SK * 64), gemv_smem(K, TB * SK),
+                           stream, x, w, s, out, N, K, norm->w, norm->bias, norm->eps);
+    else
+        hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK, false>),
+                           dim3((tiles + TB - 1) / TB), dim3(TB * SK * 64), gemv_smem(K, TB * SK),
+                           stream, x, w, s, out, N, K, nullptr, 0.0f, 0.0f);
     return hip_status(hipGetLastError(), "gemv launch");
 }
 
-/* Split-K: the smallest power of two keeping a wave at <= kMaxLoads pieces; tiles per block
- * (measured on MI355X) keep 4-8 waves per block. */
+template <bool OUT_F32, int NP>
+int launch_xwave_np(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N,
+                    int K, hipStream_t stream) {
+    constexpr int SK = kXwaveWaves;
+    hipLaunchKernelGGL((gemv_xwave_kernel<false, OUT_F32, 1, SK, NP>), dim3(N / 8), dim3(SK * 64),
+                       xwave_smem(SK, NP), stream, x, w, s, out, N, K);
+    return hip_status(hipGetLastError(), "gemv launch");
+}
+
+/* Block shapes (measured on MI355X, graph-replayed, weights rotated past the MALL):
+ * - a long K (more group pairs than one wave holds, the down projection) runs the wave-local
+ *   activation kernel with kXwaveWaves waves on one tile, NP = ceil(pairs / kXwaveWaves) each:
+ *   at K = 9728 / 8704 / 17408 it takes 5.85 / 8.35 / 14.1 us against 6.2 / 9.7 / 15.7 us for the
+ *   block-staged kernel;
+ * - otherwise the block-staged kernel, split-K being the smallest power of two that keeps a
+ *   wave at <= kMaxLoads pieces; a single-wave tile is split in two when it has more than six
+ *   pairs (K = 2560 pair operand: 8.28 against 8.56 us). */
 template <bool PAIR, bool OUT_F32>
 int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N, int K,
-                hipStream_t stream) {
+                hipStream_t stream, const NormArgs *norm = nullptr) {
     const int pairs = (K / 128 + 1) / 2;
+    if (!PAIR && !norm && pairs > kMaxLoads) {
+        switch ((pairs + kXwaveWaves - 1) / kXwaveWaves) {
+            case 1: return launch_xwave_np<OUT_F32, 1>(x, w, s, out, N, K, stream);
+            case 2: return launch_xwave_np<OUT_F32, 2>(x, w, s, out, N, K, stream);
+            case 3: return launch_xwave_np<OUT_F32, 3>(x, w, s, out, N, K, stream);
+            case 4: return launch_xwave_np<OUT_F32, 4>(x, w, s, out, N, K, stream);
+            case 5: return launch_xwave_np<OUT_F32, 5>(x, w, s, out, N, K, stream);
+            case 6: return launch_xwave_np<OUT_F32, 6>(x, w, s, out, N, K, stream);
+            case 7: return launch_xwave_np<OUT_F32, 7>(x, w, s, out, N, K, stream);
+            default: break; /* beyond the LDS slices: block-staged below */
+        }
+    }
     int sk = 1;
     while (sk < 16 && (pairs + sk - 1) / sk > kMaxLoads) sk *= 2;
     switch (sk) {
-        case 1: return launch_gemv_cfg<PAIR, OUT_F32, 4, 1>(x, w, s, out, N, K, stream);
-        case 2: return launch_gemv_cfg<PAIR, OUT_F32, 2, 2>(x, w, s, out, N, K, stream);
-        case 4: return launch_gemv_cfg<PAIR, OUT_F32, 2, 4>(x, w, s, out, N, K, stream);
-        case 8: return launch_gemv_cfg<PAIR, OUT_F32, 1, 8>(x, w, s, out, N, K, stream);
-        default: return launch_gemv_cfg<PAIR, OUT_F32, 1, 16>(x, w, s, out, N, K, stream);
+        case 1:
+            if (pairs > 6)
+                return launch_gemv_cfg<PAIR, OUT_F32, 2, 2>(x, w, s, out, N, K, stream, norm);
+            return launch_gemv_cfg<PAIR, OUT_F32, 4, 1>(x, w, s, out, N, K, stream, norm);
+        case 2: return launch_gemv_cfg<PAIR, OUT_F32, 2, 2>(x, w, s, out, N, K, stream, norm);
+        case 4: return launch_gemv_cfg<PAIR, OUT_F32, 2, 4>(x, w, s, out, N, K, stream, norm);
+        case 8: return launch_gemv_cfg<PAIR, OUT_F32, 1, 8>(x, w, s, out, N, K, stream, norm);
+        default: return launch_gemv_cfg<PAIR, OUT_F32, 1, 16>(x, w, s, out, N, K, stream, norm);
     }
 }
 
@@ -748,9 +977,9 @@ static int mlp_common(const uint16_t *normed, const uint8_t *gup, const uint16_t
     if (!act || !out) return set_error(W4A16_ERR_CONFIG, "mlp_int4: null buffer");
     int st = check_gemm_args(act, dnp, dns, out, M, hidden, inter, W4A16_GROUP, "mlp_int4 down");
     if (st < 0) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
     st = gate_up_silu_int4_bf16(normed, gup, gus, act, M, hidden, inter, stream);
     if (st) return st;
-    hipStream_t s = static_cast<hipStream_t>(stream);
     return out_f32 ? run_rows<kOutF32>(act, M, dnp, dns, out, hidden, inter, s)
                    : run_rows<kOutBf16>(act, M, dnp, dns, out, hidden, inter, s);
 }
@@ -766,6 +995,85 @@ extern "C" int mlp_int4_partial_f32(const uint16_t *normed, const uint8_t *gup,
                                     float *out_f32, uint16_t *act_ws, int M, int hidden,
                                     int inter, void *stream) {
     return mlp_common(normed, gup, gus, dnp, dns, out_f32, true, act_ws, M, hidden, inter, stream);
+}
+
+/* ---- RMSNorm and the norm-fused MLP (reference forward_mlp, csrc/kernels/layers.cu:150-159) ---- */
+
+static int norm_args(const uint16_t *w, int style, float eps, int cols, int rows, NormArgs *na,
+                     const char *what) {
+    if (rows < 0 || cols <= 0 || !std::isfinite(eps) || eps <= 0.0f)
+        return set_error(W4A16_ERR_CONFIG, "%s: invalid shape or epsilon", what);
+    if (style != 0 && style != 1)
+        return set_error(W4A16_ERR_CONFIG, "%s: norm_style %d is neither 0 (gemma) nor 1 (plain)",
+                         what, style);
+    if (rows > 0 && !w) return set_error(W4A16_ERR_CONFIG, "%s: null norm weight", what);
+    na->w = w;
+    na->bias = style == 0 ? 1.0f : 0.0f;
+    na->eps = eps;
+    return W4A16_OK;
+}
+
+extern "C" int w4a16_rmsnorm_bf16(uint16_t *out, const uint16_t *x, const uint16_t *weight,
+                                  int cols, int rows, int norm_style, float eps, void *stream) {
+    NormArgs na;
+    int st = norm_args(weight, norm_style, eps, cols, rows, &na, "w4a16_rmsnorm_bf16");
+    if (st) return st;
+    if (rows == 0) return W4A16_OK;
+    if (!out || !x) return set_error(W4A16_ERR_CONFIG, "w4a16_rmsnorm_bf16: null buffer");
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       out, x, weight, cols, na.bias, eps);
+    return hip_status(hipGetLastError(), "rmsnorm launch");
+}
+
+static int mlp_norm_common(const uint16_t *residual, const uint16_t *norm_w, int norm_style,
+                           float eps, const uint8_t *gup, const uint16_t *gus, const uint8_t *dnp,
+                           const uint16_t *dns, void *out, bool out_f32, uint16_t *ws, int M,
+                           int hidden, int inter, void *stream) {
+    if (M < 0 || hidden <= 0 || inter <= 0)
+        return set_error(W4A16_ERR_CONFIG, "mlp_int4_norm: bad extents M=%d hidden=%d inter=%d", M,
+                         hidden, inter);
+    NormArgs na;
+    int st = norm_args(norm_w, norm_style, eps, hidden, M, &na, "mlp_int4_norm");
+    if (st) return st;
+    if (M == 0) return W4A16_OK;
+    if (!residual || !ws || !out) return set_error(W4A16_ERR_CONFIG, "mlp_int4_norm: null buffer");
+    st = check_gemm_args(residual, gup, gus, ws, M, 2 * inter, hidden, W4A16_GROUP,
+                         "mlp_int4_norm gate/up");
+    if (st < 0) return st;
+    st = check_gemm_args(ws, dnp, dns, out, M, hidden, inter, W4A16_GROUP, "mlp_int4_norm down");
+    if (st < 0) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint16_t *normed = ws;                          /* [M, hidden] (M > 1) */
+    uint16_t *act = ws + (size_t)M * hidden;        /* [M, inter] */
+    if (M == 1) {
+        st = launch_gemv<true, false>(residual, gup, gus, act, 2 * inter, hidden, s, &na);
+    } else {
+        hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, s, normed, residual, norm_w,
+                           hidden, na.bias, eps);
+        st = hip_status(hipGetLastError(), "rmsnorm launch");
+        if (!st) st = run_rows<kOutPairSilu>(normed, M, gup, gus, act, 2 * inter, hidden, s);
+    }
+    if (st) return st;
+    return out_f32 ? run_rows<kOutF32>(act, M, dnp, dns, out, hidden, inter, s)
+                   : run_rows<kOutBf16>(act, M, dnp, dns, out, hidden, inter, s);
+}
+
+extern "C" int mlp_int4_norm_bf16(const uint16_t *residual, const uint16_t *norm_w,
+                                  int norm_style, float eps, const uint8_t *gup,
+                                  const uint16_t *gus, const uint8_t *dnp, const uint16_t *dns,
+                                  uint16_t *out, uint16_t *ws, int M, int hidden, int inter,
+                                  void *stream) {
+    return mlp_norm_common(residual, norm_w, norm_style, eps, gup, gus, dnp, dns, out, false, ws,
+                           M, hidden, inter, stream);
+}
+
+extern "C" int mlp_int4_norm_partial_f32(const uint16_t *residual, const uint16_t *norm_w,
+                                         int norm_style, float eps, const uint8_t *gup,
+                                         const uint16_t *gus, const uint8_t *dnp,
+                                         const uint16_t *dns, float *out_f32, uint16_t *ws, int M,
+                                         int hidden, int inter, void *stream) {
+    return mlp_norm_common(residual, norm_w, norm_style, eps, gup, gus, dnp, dns, out_f32, true,
+                           ws, M, hidden, inter, stream);
 }
 
 extern "C" int silu_mul_packed_bf16(uint16_t *out, const uint16_t *packed, int tokens, int inter,

@@ -62,6 +62,11 @@ _SIGNATURES = {
     "silu_mul_packed_bf16": (_i, [_vp, _vp, _i, _i, _vp]),
     "gate_up_silu_int4_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mlp_int4_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "w4a16_rmsnorm_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, ctypes.c_float, _vp]),
+    "mlp_int4_norm_bf16": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i,
+                                _i, _vp]),
+    "mlp_int4_norm_partial_f32": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp,
+                                       _i, _i, _i, _vp]),
     "mlp_int4_partial_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "w4a16_manifest_check": (_i, [ctypes.c_char_p, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "w4a16_artifact_verify": (_i, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _ll,
@@ -76,6 +81,9 @@ _SIGNATURES = {
     "engine_ffn_operands": (_i, [_vp, _i, _vp]),
     "engine_ffn_forward": (_i, [_vp, _i, _vp, _vp, _i, _vp]),
     "engine_ffn_forward_partial_f32": (_i, [_vp, _i, _vp, _vp, _i, _vp]),
+    "engine_ffn_forward_norm": (_i, [_vp, _i, _vp, _vp, _i, ctypes.c_float, _vp, _i, _vp]),
+    "engine_ffn_forward_norm_partial_f32": (_i, [_vp, _i, _vp, _vp, _i, ctypes.c_float, _vp, _i,
+                                                 _vp]),
     "test_gemm_int4": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i]),
     "test_silu_mul_packed": (_i, [_vp, _vp, _i, _i]),
 }
@@ -310,6 +318,37 @@ def mlp_int4(x, gu, dn, out=None, act_ws=None, partial_f32=False, stream=None):
     return out
 
 
+def rmsnorm(x, weight, norm_style, eps, out=None, stream=None):
+    """RMSNorm of the rows of x [rows, cols] (BF16 bits in int16/bfloat16 tensors)."""
+    import torch
+
+    rows, cols = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    _check(lib.w4a16_rmsnorm_bf16(out.data_ptr(), x.data_ptr(), weight.data_ptr(), cols, rows,
+                                  norm_style, eps, _stream(stream)), "w4a16_rmsnorm_bf16")
+    return out
+
+
+def mlp_int4_norm(residual, norm_w, norm_style, eps, gu, dn, out=None, ws=None, partial_f32=False,
+                  stream=None):
+    """forward_mlp: RMSNorm of residual [M, H], then the INT4 MLP."""
+    import torch
+
+    m, h = residual.shape
+    inter = gu.n // 2
+    if ws is None:
+        ws = torch.empty((m, h + inter), dtype=residual.dtype, device=residual.device)
+    if out is None:
+        out = torch.empty((m, h), dtype=torch.float32 if partial_f32 else residual.dtype,
+                          device=residual.device)
+    fn = lib.mlp_int4_norm_partial_f32 if partial_f32 else lib.mlp_int4_norm_bf16
+    _check(fn(residual.data_ptr(), norm_w.data_ptr(), norm_style, eps, gu.packed.data_ptr(),
+              gu.scales.data_ptr(), dn.packed.data_ptr(), dn.scales.data_ptr(), out.data_ptr(),
+              ws.data_ptr(), m, h, inter, _stream(stream)), "mlp_int4_norm")
+    return out
+
+
 # ----------------------------------------------------------------------------------------------
 # Sidecar and the operand store (engine_load_quantized_ffn)
 # ----------------------------------------------------------------------------------------------
@@ -400,4 +439,20 @@ class Engine:
         fn = lib.engine_ffn_forward_partial_f32 if partial_f32 else lib.engine_ffn_forward
         _check(fn(self.handle, layer, normed.data_ptr(), out.data_ptr(), m, _stream(stream)),
                "engine_ffn_forward")
+        return out
+
+    def forward_norm(self, layer, residual, norm_w, norm_style, eps, out=None, partial_f32=False,
+                     stream=None):
+        """forward_mlp: RMSNorm(residual) with norm_w (style 0 Gemma, 1 plain), then the FFN."""
+        import torch
+
+        m = residual.shape[0]
+        if out is None:
+            out = torch.empty((m, self.hidden),
+                              dtype=torch.float32 if partial_f32 else residual.dtype,
+                              device=residual.device)
+        fn = (lib.engine_ffn_forward_norm_partial_f32 if partial_f32
+              else lib.engine_ffn_forward_norm)
+        _check(fn(self.handle, layer, residual.data_ptr(), norm_w.data_ptr(), norm_style, eps,
+                  out.data_ptr(), m, _stream(stream)), "engine_ffn_forward_norm")
         return out

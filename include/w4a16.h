@@ -132,6 +132,30 @@ int mlp_int4_partial_f32(const uint16_t *normed, const uint8_t *gu_packed,
                          const uint16_t *dn_scales, float *out_f32, uint16_t *act_ws, int M,
                          int hidden, int intermediate, void *stream);
 
+/* RMSNorm of `rows` rows of `cols` BF16 values: out = BF16(x * rsqrt(mean(x^2) + eps) * (b + w)),
+ * b = 1 for norm_style 0 (Gemma, weight + 1) and 0 for norm_style 1 (plain), FP32 arithmetic.
+ * Replaces kernel_gemma_rms_norm / kernel_rms_norm_plain (reference
+ * csrc/kernels/flashinfer_norm.cu:22-76, chosen by layer_norm, csrc/kernels/layers.cu:16-25),
+ * with their refusals (rows < 0, cols <= 0, eps not finite and positive; rows == 0 no-op). */
+int w4a16_rmsnorm_bf16(uint16_t *out, const uint16_t *x, const uint16_t *weight, int cols,
+                       int rows, int norm_style, float eps, void *stream);
+
+/* forward_mlp (reference csrc/kernels/layers.cu:150-159): the post-attention RMSNorm of the
+ * residual [M, hidden], then the INT4 MLP. At M = 1 the norm is formed inside the gate/up
+ * kernel's activation staging (no separate launch, no normed round trip); M > 1 normalises
+ * into ws first. ws: M * (hidden + intermediate) BF16 (normed, then act). */
+int mlp_int4_norm_bf16(const uint16_t *residual, const uint16_t *norm_w, int norm_style,
+                       float eps, const uint8_t *gu_packed, const uint16_t *gu_scales,
+                       const uint8_t *dn_packed, const uint16_t *dn_scales, uint16_t *out,
+                       uint16_t *ws, int M, int hidden, int intermediate, void *stream);
+
+/* Same, with the tensor-parallel FP32 partial of the down projection (as mlp_int4_partial_f32). */
+int mlp_int4_norm_partial_f32(const uint16_t *residual, const uint16_t *norm_w, int norm_style,
+                              float eps, const uint8_t *gu_packed, const uint16_t *gu_scales,
+                              const uint8_t *dn_packed, const uint16_t *dn_scales,
+                              float *out_f32, uint16_t *ws, int M, int hidden, int intermediate,
+                              void *stream);
+
 /* ---------------------------------------------------------------------------------------
  * Sidecar and artifacts (host). Status values are the reference reader's QuantManifestStatus
  * (reference csrc/include/quant_manifest.h:55-63): 0 ok, 1 arg, 2 syntax, 3 format, 4 shape,
@@ -215,6 +239,17 @@ int engine_ffn_forward(EngineHandle *engine, int layer, const uint16_t *normed, 
                        int tokens, void *stream);
 int engine_ffn_forward_partial_f32(EngineHandle *engine, int layer, const uint16_t *normed,
                                    float *out, int tokens, void *stream);
+
+/* forward_mlp (reference csrc/kernels/layers.cu:150-159) on a loaded layer: the post-attention
+ * RMSNorm of residual [tokens, hidden] with the caller's norm weight (LayerWeights::post_norm_w,
+ * kept by the engine with its BF16 weights; style and eps as ModelDims::norm_style / rms_eps),
+ * then the INT4 MLP (see mlp_int4_norm_bf16). */
+int engine_ffn_forward_norm(EngineHandle *engine, int layer, const uint16_t *residual,
+                            const uint16_t *norm_w, int norm_style, float eps, uint16_t *out,
+                            int tokens, void *stream);
+int engine_ffn_forward_norm_partial_f32(EngineHandle *engine, int layer, const uint16_t *residual,
+                                        const uint16_t *norm_w, int norm_style, float eps,
+                                        float *out, int tokens, void *stream);
 
 /* ---------------------------------------------------------------------------------------
  * Test bridges (host pointers, artifact layout; synchronous).

@@ -43,6 +43,7 @@ def _load():
         "orc_silu_mul_packed": (ctypes.c_int, [_ll, _ll, _vp, _vp]),
         "orc_ffn_bf16": (ctypes.c_int, [_ll, _ll, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
         "orc_ffn_partial_f32": (ctypes.c_int, [_ll, _ll, _ll, _vp, _vp, _vp, _vp, _vp, _vp]),
+        "orc_rmsnorm_bf16": (ctypes.c_int, [_ll, _ll, _vp, _vp, ctypes.c_int, ctypes.c_double, _vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -154,6 +155,24 @@ def ffn_partial_f32(x_bits, gu_packed, gu_scales, dn_packed, dn_scales, hidden, 
                                 _p(_c(gu_scales, np.uint16)), _p(_c(dn_packed, np.uint8)),
                                 _p(_c(dn_scales, np.uint16)), _p(out)), "ffn_partial_f32")
     return out
+
+
+def rmsnorm_bf16(x_bits, w_bits, norm_style, eps):
+    """BF16 bits [rows, cols]: x * rsqrt(mean(x^2) + eps) * (bias + w), bias 1 for norm_style 0
+    (Gemma) and 0 for 1 (plain)."""
+    x = _c(x_bits, np.uint16)
+    rows, cols = (1, x.shape[0]) if x.ndim == 1 else x.shape
+    out = np.zeros((rows, cols), np.uint16)
+    _ok(lib.orc_rmsnorm_bf16(rows, cols, _p(x), _p(_c(w_bits, np.uint16)), norm_style, eps,
+                             _p(out)), "rmsnorm_bf16")
+    return out
+
+
+def lib_rmsnorm_raw(cols, eps, norm_style, rows=1):
+    """The refusal path only: call with placeholder buffers."""
+    x = np.zeros(max(cols, 1) * max(rows, 1), np.uint16)
+    out = np.zeros_like(x)
+    _ok(lib.orc_rmsnorm_bf16(rows, cols, _p(x), _p(x), norm_style, eps, _p(out)), "rmsnorm_bf16")
 
 
 # ---- numpy restatement of the reference test's dequantizer and the CPU baseline ------------------

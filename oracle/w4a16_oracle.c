@@ -246,3 +246,31 @@ int orc_ffn_partial_f32(long long m, long long h, long long inter, const uint16_
     free(od);
     return st;
 }
+
+/* reference csrc/kernels/flashinfer_norm.cu:22-76 (FlashInfer RMSNorm / GemmaRMSNorm). */
+int orc_rmsnorm_bf16(long long rows, long long cols, const uint16_t *x, const uint16_t *w,
+                     int norm_style, double eps, uint16_t *out) {
+    if (rows < 0 || cols <= 0 || !isfinite(eps) || eps <= 0.0)
+        return fail(ORC_ERR_RANGE, "invalid shape or epsilon");
+    if (rows == 0) return ORC_OK;
+    if (!x || !w || !out) return fail(ORC_ERR_ARG, "null argument");
+    if (norm_style != 0 && norm_style != 1) return fail(ORC_ERR_ARG, "norm_style must be 0 or 1");
+    const double bias = norm_style == 0 ? 1.0 : 0.0;
+    for (long long r = 0; r < rows; ++r) {
+        const uint16_t *xr = x + r * cols;
+        double ss = 0.0;
+        for (long long c = 0; c < cols; ++c) {
+            const double v = orc_bf16_to_f32(xr[c]);
+            ss += v * v;
+        }
+        /* the scale in double, rounded once to FP32; then FlashInfer's FP32 products in its
+         * order, x * rms first, then times (bias + w) */
+        const float rms = (float)(1.0 / sqrt(ss / (double)cols + eps));
+        for (long long c = 0; c < cols; ++c) {
+            const float xs = orc_bf16_to_f32(xr[c]) * rms;
+            const float wb = (float)bias + orc_bf16_to_f32(w[c]);
+            out[r * cols + c] = orc_f32_to_bf16(xs * wb);
+        }
+    }
+    return ORC_OK;
+}

@@ -89,6 +89,19 @@ int orc_ffn_partial_f32(long long m, long long hidden, long long inter, const ui
                         const uint8_t *gu_packed, const uint16_t *gu_scales,
                         const uint8_t *dn_packed, const uint16_t *dn_scales, float *out_f32);
 
+/* RMSNorm ahead of the FFN (reference csrc/kernels/layers.cu:16-25,150-159, which calls
+ * kernel_rms_norm_plain / kernel_gemma_rms_norm, csrc/kernels/flashinfer_norm.cu:22-76, i.e.
+ * FlashInfer 0.5.3 norm::RMSNorm / GemmaRMSNorm, a third-party header absent from the
+ * reference tree). Its published algorithm:
+ *   out[r, c] = BF16( x[r, c] * rsqrt(sum_c x[r, c]^2 / cols + eps) * (bias + w[c]) )
+ * with bias = 1 for norm_style 0 (Gemma: weight + 1) and 0 for norm_style 1 (plain), all in
+ * FP32 there. Here the sum of squares and the root are taken in double and rounded once to
+ * FP32 (any FP32 summation order is within an FP32 ULP of it); the two products are FP32 in
+ * FlashInfer's order ((x * rms) * (bias + w)), then BF16 RNE. Refuses rows < 0, cols <= 0 and an
+ * epsilon that is not finite and positive (flashinfer_norm.cu:25-27). */
+int orc_rmsnorm_bf16(long long rows, long long cols, const uint16_t *x_bf16,
+                     const uint16_t *w_bf16, int norm_style, double eps, uint16_t *out_bf16);
+
 #ifdef __cplusplus
 }
 #endif

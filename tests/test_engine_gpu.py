@@ -79,6 +79,14 @@ def test_load_and_forward_tp1(cuda, model):
         got = eng.forward(layer, xd).cpu().numpy().view(np.uint16)
         ref, _, _ = oracle.ffn_bf16(x, gup, gus, dp, ds, H, I)
         assert_parity(got, ref, f"engine layer {layer}", floor_div=16.0)
+        # forward_mlp: the post-attention RMSNorm folded in (plain style, eps 1e-6)
+        print(f"engine tp=1 forward_norm layer {layer}", flush=True)
+        nw = oracle.bf16_bits(np.random.default_rng(layer).normal(1.0, 0.2, H).astype(np.float32))
+        got = eng.forward_norm(layer, xd, torch.from_numpy(nw.view(np.int16)).to(cuda), 1, 1e-6)
+        normed = oracle.rmsnorm_bf16(x, nw, 1, 1e-6)
+        ref, _, _ = oracle.ffn_bf16(normed, gup, gus, dp, ds, H, I)
+        assert_parity(got.cpu().numpy().view(np.uint16), ref, f"engine norm layer {layer}",
+                      floor_div=16.0)
     eng.close()
 
 

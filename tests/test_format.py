@@ -120,3 +120,26 @@ def test_test_bridge_refuses_k192_without_touching_the_device():
     st = w4a16.lib.test_gemm_int4(out.ctypes.data, out.ctypes.data, bad.ctypes.data,
                                   sc.ctypes.data, 1, 128, 192, 128)
     assert st != 0
+
+
+def test_norm_entry_refusals_without_touching_the_device():
+    """w4a16_rmsnorm_bf16 / mlp_int4_norm_bf16 refuse as the reference's norm wrappers do
+    (csrc/kernels/flashinfer_norm.cu:25-31: rows < 0, cols <= 0, eps not finite and positive;
+    rows == 0 is a no-op) plus an unknown norm_style, before any device call."""
+    lib = w4a16.lib
+    dummy = 16  # a non-null address that is never dereferenced on these paths
+    for cols, rows, style, eps in ((0, 1, 0, 1e-6), (256, -1, 0, 1e-6), (256, 1, 0, 0.0),
+                                   (256, 1, 0, float("inf")), (256, 1, 2, 1e-6)):
+        assert lib.w4a16_rmsnorm_bf16(dummy, dummy, dummy, cols, rows, style, eps, None) == \
+            w4a16.W4A16_ERR_CONFIG
+    assert "epsilon" in w4a16.last_error() or "norm_style" in w4a16.last_error()
+    assert lib.w4a16_rmsnorm_bf16(None, None, None, 256, 0, 1, 1e-6, None) == w4a16.W4A16_OK
+    args = (dummy, dummy, dummy, dummy, dummy, dummy)
+    assert lib.mlp_int4_norm_bf16(dummy, dummy, 1, -1.0, *args, 1, 2560, 9728, None) == \
+        w4a16.W4A16_ERR_CONFIG
+    assert lib.mlp_int4_norm_bf16(dummy, dummy, 3, 1e-6, *args, 1, 2560, 9728, None) == \
+        w4a16.W4A16_ERR_CONFIG
+    assert lib.mlp_int4_norm_bf16(dummy, None, 1, 1e-6, *args, 1, 2560, 9728, None) == \
+        w4a16.W4A16_ERR_CONFIG
+    assert lib.mlp_int4_norm_bf16(dummy, dummy, 1, 1e-6, *args, 0, 2560, 9728, None) == \
+        w4a16.W4A16_OK

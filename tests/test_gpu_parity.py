@@ -190,6 +190,66 @@ def test_ffn_parity(cuda, hidden, inter, m):
     assert_parity(out, ref, f"ffn H={hidden} I={inter} M={m}", floor_div=16.0)
 
 
+def norm_inputs(rows, hidden, style, seed):
+    """A residual with a spread of row scales and a norm weight of the style's shape (Gemma
+    weights are offsets around 0, plain ones gains around 1)."""
+    rng = np.random.default_rng(seed)
+    x = oracle.bf16_to_f32(oracle.synth_activation(rows, hidden, seed))
+    x *= np.float32(2.0) ** rng.integers(-3, 4, size=(rows, 1)).astype(np.float32)
+    w = rng.normal(0.0 if style == 0 else 1.0, 0.2, hidden).astype(np.float32)
+    return oracle.bf16_bits(x), oracle.bf16_bits(w)
+
+
+def ulp_diff(a, b):
+    """|a - b| in BF16 ULPs of the larger magnitude (sign-magnitude bit patterns)."""
+    ia = np.where(a & 0x8000, -(a & 0x7FFF).astype(np.int64), (a & 0x7FFF).astype(np.int64))
+    ib = np.where(b & 0x8000, -(b & 0x7FFF).astype(np.int64), (b & 0x7FFF).astype(np.int64))
+    return np.abs(ia - ib)
+
+
+@pytest.mark.parametrize("style", [0, 1])
+def test_rmsnorm_parity(cuda, style):
+    """w4a16_rmsnorm_bf16 against the oracle: within 1 BF16 ULP everywhere (the FP32 sum of
+    squares is ordered differently from the oracle's double), and bit-exact for >= 99%."""
+    for rows, hidden in ((1, 2560), (5, 5120), (16, 2560)):
+        say(f"rmsnorm style={style} rows={rows} H={hidden}")
+        x, w = norm_inputs(rows, hidden, style, seed=40 + rows)
+        got = from_dev(w4a16.rmsnorm(to_dev(x, cuda), to_dev(w, cuda), style, 1e-6))
+        want = oracle.rmsnorm_bf16(x, w, style, 1e-6)
+        d = ulp_diff(got, want)
+        assert d.max() <= 1, (rows, hidden, int(d.max()))
+        assert np.mean(d == 0) >= 0.99
+
+
+@pytest.mark.parametrize("style", [0, 1])
+@pytest.mark.parametrize("m", [1, 2, 16])
+def test_ffn_norm_parity(cuda, style, m):
+    """mlp_int4_norm (forward_mlp, reference csrc/kernels/layers.cu:150-159) against the
+    oracle's RMSNorm followed by the oracle FFN, at the end-to-end bar of test_ffn_parity; at
+    M = 1 the norm runs inside the gate/up kernel, at M > 1 in its own kernel ahead of the MFMA
+    form. The FP32 partial form is checked against the oracle's unrounded partial."""
+    hidden, inter = 2560, 9728
+    say(f"ffn norm style={style} M={m}")
+    gup, gus, dp, ds = make_ffn(hidden, inter)
+    x, w = norm_inputs(m, hidden, style, seed=60 + m)
+    gu = w4a16.TiledWeight.from_artifact(gup, gus, 2 * inter, hidden, pair=True, device=cuda)
+    dn = w4a16.TiledWeight.from_artifact(dp, ds, hidden, inter, device=cuda)
+    xd, wd = to_dev(x, cuda), to_dev(w, cuda)
+    import torch
+
+    ws = torch.empty((m, hidden + inter), dtype=xd.dtype, device=cuda)
+    out = from_dev(w4a16.mlp_int4_norm(xd, wd, style, 1e-6, gu, dn, ws=ws))
+    normed = oracle.rmsnorm_bf16(x, w, style, 1e-6)
+    ref, _, ref_act = oracle.ffn_bf16(normed, gup, gus, dp, ds, hidden, inter)
+    act = from_dev(ws.reshape(-1)[m * hidden:].reshape(m, inter))  # ws = normed | act
+    assert_parity(act, ref_act, f"ffn norm act stage M={m}", floor_div=16.0)
+    assert_parity(out, ref, f"ffn norm H={hidden} I={inter} M={m}", floor_div=16.0)
+    part = from_dev(w4a16.mlp_int4_norm(xd, wd, style, 1e-6, gu, dn, partial_f32=True))
+    want = oracle.ffn_partial_f32(normed, gup, gus, dp, ds, hidden, inter)
+    rel = np.linalg.norm(part.astype(np.float64) - want) / np.linalg.norm(want)
+    assert rel <= 1e-3, rel
+
+
 def test_ffn_tp_slice_partial_f32(cuda):
     """Config 4: rank 0 of tp=2 on the 27B FFN, scales kept global (reference
     csrc/engine.cu:2308-2369: gate/up rows 0..I/2-1 of each half, down columns 0..I/2-1)."""

@@ -248,3 +248,45 @@ def test_ffn_recomposes_from_stages():
     base = oracle.ffn_cpu_baseline(x, gp, gs, dp, ds, h, inter)
     d = np.abs(oracle.bf16_to_f32(base) - oracle.bf16_to_f32(out))
     assert d.max() <= 2 ** -6 * np.abs(oracle.bf16_to_f32(out)).max()
+
+
+def test_rmsnorm_closed_forms():
+    """orc_rmsnorm_bf16 against values the formula fixes exactly (FlashInfer RMSNorm behind
+    reference csrc/kernels/flashinfer_norm.cu:22-76; bias 1 for norm_style 0 = Gemma):
+
+    * a constant row c with eps negligible normalises to sign(c): out = BF16(b + w) exactly,
+      pinning the mean (a sum would scale by 1/sqrt(cols)) and the bias per style;
+    * c = 1, eps = 3 gives rsqrt(1 + 3) = 1/2 exactly: eps is added to the mean inside the root;
+    * a zero row gives zeros (eps keeps the root positive);
+    * scaling a row by a power of two leaves the output bit-identical (homogeneity);
+    * a one-hot row v e_j with eps negligible gives sqrt(cols) * sign(v) * (b + w_j) at j.
+    """
+    cols = 256
+    rng = np.random.default_rng(5)
+    w = oracle.bf16_bits(rng.normal(0.0, 0.25, cols).astype(np.float32))
+    wf = oracle.bf16_to_f32(w).astype(np.float64)
+    for style, bias in ((0, 1.0), (1, 0.0)):
+        want = oracle.bf16_bits((bias + wf).astype(np.float32))
+        for c in (2.0, -0.375, 96.0):
+            x = oracle.bf16_bits(np.full(cols, c, np.float32))
+            got = oracle.rmsnorm_bf16(x, w, style, 1e-20)[0]
+            expect = want if c > 0 else oracle.bf16_bits(-(bias + wf).astype(np.float32))
+            assert np.array_equal(got, expect), (style, c)
+        x = oracle.bf16_bits(np.ones(cols, np.float32))
+        got = oracle.rmsnorm_bf16(x, w, style, 3.0)[0]
+        assert np.array_equal(got, oracle.bf16_bits((0.5 * (bias + wf)).astype(np.float32)))
+        zero = oracle.rmsnorm_bf16(np.zeros(cols, np.uint16), w, style, 1e-6)[0]
+        assert not np.any(zero & 0x7FFF)
+        xr = oracle.synth_activation(3, cols, seed=9)
+        scaled = oracle.bf16_bits(oracle.bf16_to_f32(xr) * np.float32(8.0))
+        assert np.array_equal(oracle.rmsnorm_bf16(xr, w, style, 1e-20),
+                              oracle.rmsnorm_bf16(scaled, w, style, 1e-20))
+        onehot = np.zeros(cols, np.uint16)
+        onehot[17] = oracle.bf16_bits(np.float32([-3.0]))[0]
+        got = oracle.rmsnorm_bf16(onehot, w, style, 1e-20)[0]
+        assert got[17] == oracle.bf16_bits(np.float32([-16.0 * (bias + wf[17])]))[0]
+        assert not np.any(np.delete(got, 17) & 0x7FFF)
+    for bad in ((0, 1e-6, 0), (cols, 0.0, 0), (cols, float("nan"), 0), (cols, 1e-6, 2)):
+        c_, eps, style = bad
+        with pytest.raises(oracle.OracleError):
+            oracle.lib_rmsnorm_raw(c_, eps, style)
