@@ -171,6 +171,9 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
      * BF16(x * rsqrt(sum x^2 / K + eps) * (norm_bias + w)), the FP32 order of the reference's
      * norm (FlashInfer RMSNorm / GemmaRMSNorm behind csrc/kernels/flashinfer_norm.cu:22-76) */
     if (NORM) {
+        /* keep the weight loads above: without this fence the scheduler hoists the sum of
+         * squares over them, and the weights would wait for the activation's round trip */
+        __builtin_amdgcn_sched_barrier(0);
         float ss = 0.0f;
 #pragma unroll
         for (int it = 0; it < kXIters; ++it) {
@@ -200,7 +203,10 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
                                  (norm_bias + bf16_widen((uint16_t)(n4[q] & 0xFFFFu)));
                 const float hi = bf16_widen((uint16_t)(w4[q] >> 16)) * rms *
                                  (norm_bias + bf16_widen((uint16_t)(n4[q] >> 16)));
-                w4[q] = (uint32_t)bf16_rne(lo) | ((uint32_t)bf16_rne(hi) << 16);
+                /* v_cvt_pk_bf16_f32: round-to-nearest-even of both, packed (finite values:
+                 * the same bits as bf16_rne) */
+                const bf16x2_t packed = {(__bf16)lo, (__bf16)hi};
+                w4[q] = __builtin_bit_cast(uint32_t, packed);
             }
             xv[it] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
         }
@@ -775,7 +781,8 @@ int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *ou
     while (sk < 16 && (pairs + sk - 1) / sk > kMaxLoads) sk *= 2;
     switch (sk) {
         case 1:
-            if (pairs > 6)
+            /* with the RMSNorm prologue every block normalises all of x: fewer, larger blocks */
+            if (pairs > 6 && !norm)
                 return launch_gemv_cfg<PAIR, OUT_F32, 2, 2>(x, w, s, out, N, K, stream, norm);
             return launch_gemv_cfg<PAIR, OUT_F32, 4, 1>(x, w, s, out, N, K, stream, norm);
         case 2: return launch_gemv_cfg<PAIR, OUT_F32, 2, 2>(x, w, s, out, N, K, stream, norm);
