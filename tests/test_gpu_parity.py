@@ -98,7 +98,10 @@ def test_quantize_device_bit_exact(cuda):
 # ---- GEMV (gemm_int4_bf16, M = 1) ----------------------------------------------------------------
 
 @pytest.mark.parametrize("n,k", [(9728, 2560), (2560, 9728), (5120, 17408), (8704, 5120),
-                                 (256, 128), (1024, 384), (24, 1152)])
+                                 (256, 128), (1024, 384), (24, 1152),
+                                 # wave-local kernel with an odd group count (13 pairs, NP = 1),
+                                 # its widest slice (NP = 7), and past it (block-staged, SK = 16)
+                                 (64, 3200), (40, 28672), (16, 30464)])
 def test_gemv_parity(cuda, n, k):
     say(f"gemv n={n} k={k}")
     p, s = make_weight(n, k, seed=n + k)
@@ -107,6 +110,19 @@ def test_gemv_parity(cuda, n, k):
     out = from_dev(w4a16.gemm_int4_bf16(to_dev(x, cuda), w))
     ref = oracle.gemm_bf16(x, p, s, n, k)
     assert_parity(out, ref, f"gemv {n}x{k}")
+
+
+@pytest.mark.parametrize("m", [3, 5, 7, 13, 17, 40])
+def test_small_m_parity(cuda, m):
+    """The MFMA form at row counts between the instantiated ones (3, 5, 7, 13 take the 4-row
+    and 16-row A layouts with zero rows) and past 16 (17 and 40 run 16-row slices)."""
+    n, k = 2560, 3200  # odd group count: the last group pair is half empty
+    say(f"gemm M={m} n={n} k={k}")
+    p, s = make_weight(n, k, seed=77)
+    x = oracle.synth_activation(m, k, seed=100 + m)
+    w = w4a16.TiledWeight.from_artifact(p, s, n, k, device=cuda)
+    out = from_dev(w4a16.gemm_int4_bf16(to_dev(x, cuda), w))
+    assert_parity(out, oracle.gemm_bf16(x, p, s, n, k), f"gemm M={m}")
 
 
 def test_gemv_closed_forms(cuda):
