@@ -258,12 +258,13 @@ def main():
         dom_name = f"{family} (fused gate/up + SiLU x up)"
     achieved = dom_bytes / (k1_avg * 1e-6) / 1e9
     traffic, traffic_src = None, None
-    tpath = os.path.join(ROOT, "profiles", f"traffic_config{args.config}.json")
+    tag = f"config{args.config}" + (f"_m{m}" if args.config == 3 else "")
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{tag}.json")
     if os.path.exists(tpath):
         # HBM bytes per launch of this kernel from the committed rocprofv3 --pmc summary
         # (FETCH_SIZE and WRITE_SIZE scaled by a plain copy of known size).
         with open(tpath) as handle:
-            entries = json.load(handle).get(f"config{args.config}", {})
+            entries = json.load(handle).get(tag, {})
         prefix = ("gemv_tiles_kernel<false, false" if linear_only else "gemv_tiles_kernel<true, false")
         if m != 1:
             prefix = "mfma_gemm_kernel<0" if linear_only else "mfma_gemm_kernel<1"

@@ -598,18 +598,36 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
 }
 
 /* RMSNorm of each row (one block a row): BF16(x * rsqrt(sum x^2 / cols + eps) * (bias + w)),
- * FP32 arithmetic (reference csrc/kernels/flashinfer_norm.cu:22-76). */
+ * FP32 arithmetic (reference csrc/kernels/flashinfer_norm.cu:22-76). Each thread holds CH
+ * 8-value chunks of the row, all loaded before any use, so a row costs one load round trip;
+ * cols % 8 == 0 and cols <= CH * 8 * 256 (the launcher checks). */
+template <int CH>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t *__restrict__ out,
                                                       const uint16_t *__restrict__ x,
                                                       const uint16_t *__restrict__ w, int cols,
                                                       float bias, float eps) {
     __shared__ float red[4];
-    const uint16_t *xr = x + (size_t)blockIdx.x * cols;
-    uint16_t *orow = out + (size_t)blockIdx.x * cols;
+    const int chunks = cols >> 3;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + (size_t)blockIdx.x * cols, (uint32_t)cols * 2);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w, (uint32_t)cols * 2);
+    uint4 xv[CH], wv[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 256 + threadIdx.x;
+        xv[c] = buf_load16(xr, i < chunks ? (uint32_t)i * 16 : kOob);
+        wv[c] = buf_load16(wr, i < chunks ? (uint32_t)i * 16 : kOob);
+    }
     float ss = 0.0f;
-    for (int c = threadIdx.x; c < cols; c += 256) {
-        const float v = bf16_widen(xr[c]);
-        ss = fmaf(v, v, ss);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const uint32_t w4[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float lo = bf16_widen((uint16_t)(w4[q] & 0xFFFFu));
+            const float hi = bf16_widen((uint16_t)(w4[q] >> 16));
+            ss = fmaf(lo, lo, ss);
+            ss = fmaf(hi, hi, ss);
+        }
     }
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
@@ -617,8 +635,24 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t *__restrict__ out
     __syncthreads();
     const float total = red[0] + red[1] + red[2] + red[3];
     const float rms = 1.0f / sqrtf(total / (float)cols + eps);
-    for (int c = threadIdx.x; c < cols; c += 256)
-        orow[c] = bf16_rne(bf16_widen(xr[c]) * rms * (bias + bf16_widen(w[c])));
+    uint4 *orow = reinterpret_cast<uint4 *>(out + (size_t)blockIdx.x * cols);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 256 + threadIdx.x;
+        const uint32_t x4[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+        const uint32_t n4[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+        uint32_t o4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float lo = bf16_widen((uint16_t)(x4[q] & 0xFFFFu)) * rms *
+                             (bias + bf16_widen((uint16_t)(n4[q] & 0xFFFFu)));
+            const float hi = bf16_widen((uint16_t)(x4[q] >> 16)) * rms *
+                             (bias + bf16_widen((uint16_t)(n4[q] >> 16)));
+            const bf16x2_t packed = {(__bf16)lo, (__bf16)hi};
+            o4[q] = __builtin_bit_cast(uint32_t, packed);
+        }
+        if (i < chunks) orow[i] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+    }
 }
 
 __global__ void silu_mul_packed_kernel(uint16_t *__restrict__ out,
@@ -1020,6 +1054,19 @@ static int norm_args(const uint16_t *w, int style, float eps, int cols, int rows
     return W4A16_OK;
 }
 
+static int launch_rmsnorm(uint16_t *out, const uint16_t *x, const uint16_t *w, int cols, int rows,
+                          float bias, float eps, hipStream_t s) {
+    const int ch = (cols / 8 + 255) / 256;
+    if (cols % 8 || ch > 8)
+        return set_error(W4A16_ERR_CONFIG, "rmsnorm: cols=%d must be a multiple of 8 and <= 16384",
+                         cols);
+    if (ch <= 1) hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(rows), dim3(256), 0, s, out, x, w, cols, bias, eps);
+    else if (ch <= 2) hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3(rows), dim3(256), 0, s, out, x, w, cols, bias, eps);
+    else if (ch <= 4) hipLaunchKernelGGL(rmsnorm_kernel<4>, dim3(rows), dim3(256), 0, s, out, x, w, cols, bias, eps);
+    else hipLaunchKernelGGL(rmsnorm_kernel<8>, dim3(rows), dim3(256), 0, s, out, x, w, cols, bias, eps);
+    return hip_status(hipGetLastError(), "rmsnorm launch");
+}
+
 extern "C" int w4a16_rmsnorm_bf16(uint16_t *out, const uint16_t *x, const uint16_t *weight,
                                   int cols, int rows, int norm_style, float eps, void *stream) {
     NormArgs na;
@@ -1027,9 +1074,7 @@ extern "C" int w4a16_rmsnorm_bf16(uint16_t *out, const uint16_t *x, const uint16
     if (st) return st;
     if (rows == 0) return W4A16_OK;
     if (!out || !x) return set_error(W4A16_ERR_CONFIG, "w4a16_rmsnorm_bf16: null buffer");
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream),
-                       out, x, weight, cols, na.bias, eps);
-    return hip_status(hipGetLastError(), "rmsnorm launch");
+    return launch_rmsnorm(out, x, weight, cols, rows, na.bias, eps, static_cast<hipStream_t>(stream));
 }
 
 static int mlp_norm_common(const uint16_t *residual, const uint16_t *norm_w, int norm_style,
@@ -1052,12 +1097,14 @@ static int mlp_norm_common(const uint16_t *residual, const uint16_t *norm_w, int
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint16_t *normed = ws;                          /* [M, hidden] (M > 1) */
     uint16_t *act = ws + (size_t)M * hidden;        /* [M, inter] */
-    if (M == 1) {
+    /* The prologue costs every gate/up block a normalisation of the whole row, so it pays only
+     * while a block's waves each hold all of K (measured at H = 2560: 16.2 us per norm + FFN
+     * call fused, 17.8 us with a separate norm launch); at H = 5120 the separate launch is
+     * cheaper (35.0 against 38.4 us). */
+    if (M == 1 && (hidden / W4A16_GROUP + 1) / 2 <= kMaxLoads) {
         st = launch_gemv<true, false>(residual, gup, gus, act, 2 * inter, hidden, s, &na);
     } else {
-        hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, s, normed, residual, norm_w,
-                           hidden, na.bias, eps);
-        st = hip_status(hipGetLastError(), "rmsnorm launch");
+        st = launch_rmsnorm(normed, residual, norm_w, hidden, M, na.bias, eps, s);
         if (!st) st = run_rows<kOutPairSilu>(normed, M, gup, gus, act, 2 * inter, hidden, s);
     }
     if (st) return st;

@@ -136,7 +136,8 @@ int mlp_int4_partial_f32(const uint16_t *normed, const uint8_t *gu_packed,
  * b = 1 for norm_style 0 (Gemma, weight + 1) and 0 for norm_style 1 (plain), FP32 arithmetic.
  * Replaces kernel_gemma_rms_norm / kernel_rms_norm_plain (reference
  * csrc/kernels/flashinfer_norm.cu:22-76, chosen by layer_norm, csrc/kernels/layers.cu:16-25),
- * with their refusals (rows < 0, cols <= 0, eps not finite and positive; rows == 0 no-op). */
+ * with their refusals (rows < 0, cols <= 0, eps not finite and positive; rows == 0 no-op), plus
+ * this kernel's own: cols a multiple of 8 and at most 16384, rows 16-byte aligned. */
 int w4a16_rmsnorm_bf16(uint16_t *out, const uint16_t *x, const uint16_t *weight, int cols,
                        int rows, int norm_style, float eps, void *stream);
 
