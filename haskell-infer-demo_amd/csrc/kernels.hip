@@ -278,30 +278,36 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
  * activation of its own group pairs (512 bytes a pair, 8 bytes a lane, issued with its weight
  * loads) into a private LDS slice, and forms the per-(group, kb) sums with shuffles. No block
  * barrier stands between a wave's loads and its dot products, so a wave starts as soon as its
- * own data arrives; the only barrier is the final split-K reduction. Suits a long K (the down
- * projection), where staging the whole activation per block costs a round trip before any
- * compute can start. NP: group pairs per wave (SK * NP >= pairs). */
-template <bool PAIR, bool OUT_F32, int TB, int SK, int NP>
-__global__ __launch_bounds__(TB * SK * 64) void gemv_xwave_kernel(
+ * own data arrives. Suits a long K (the down projection), where staging the whole activation per
+ * block costs a round trip before any compute can start.
+ *
+ * One 8-row tile is split over BS blocks of SK waves: global wave gw = part * SK + wave takes
+ * the group pairs gw + i * SK * BS (i < NP). The SK waves of a block meet in LDS; with BS > 1 the
+ * blocks of a tile store FP32 row partials with agent-scope stores, count on the tile's
+ * agent-scope counter, and the last to arrive adds the BS partials in block order (independent
+ * of arrival order), writes the row and resets the counter. */
+template <bool OUT_F32, int SK, int NP, int BS>
+__global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ wt,
-    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K) {
-    constexpr int W = TB * SK;
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, float *partial,
+    unsigned *counters) {
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
     const int P = (G + 1) >> 1;
-    const int tiles = N >> 3;
+    const int tile = blockIdx.x / BS;
+    const int part = blockIdx.x % BS;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int tile = blockIdx.x * TB + wave / SK;
-    const int ks = wave % SK;
+    const int gw = part * SK + wave;
+    constexpr int kStride = SK * BS;
     const int half = lane >> 5;
     const int piece = lane & 31;
     const int kb = piece >> 3;
     const int r = piece & 7;
     uint4 *xslice = smem4 + wave * NP * 32; /* pair i: 32 chunks of 16 bytes */
-    float *red = reinterpret_cast<float *>(smem4 + W * NP * 32);
+    float *red = reinterpret_cast<float *>(smem4 + SK * NP * 32);
 
     /* 1. this wave's activation (pair p: values [256 p, 256 p + 256), lane l holds 4 l..4 l+3),
      * then its weight pieces and scales */
@@ -309,22 +315,19 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_xwave_kernel(
     uint2 xv[NP];
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-        const int p = ks + i * SK;
+        const int p = gw + i * kStride;
         const auto v = __builtin_amdgcn_raw_buffer_load_b64(
             xr, p < P ? (int)(p * 512 + lane * 8) : (int)kOob, 0, 0);
         xv[i] = __builtin_bit_cast(uint2, v);
     }
-    const bool tile_ok = tile < tiles;
     const size_t tile_bytes = (size_t)G * 512;
-    const __amdgpu_buffer_rsrc_t wr =
-        make_rsrc(wt + (size_t)(tile_ok ? tile : 0) * tile_bytes, tile_ok ? (uint32_t)tile_bytes : 0);
-    const __amdgpu_buffer_rsrc_t sr =
-        make_rsrc(st + (size_t)(tile_ok ? tile : 0) * G * 8, tile_ok ? (uint32_t)G * 16 : 0);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wt + (size_t)tile * tile_bytes, (uint32_t)tile_bytes);
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(st + (size_t)tile * G * 8, (uint32_t)G * 16);
     uint4 buf[NP];
     uint16_t sbits[NP];
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-        const int p = ks + i * SK;
+        const int p = gw + i * kStride;
         const int g = 2 * p + half;
         const bool ok = p < P && g < G;
         buf[i] = buf_load16(wr, ok ? (uint32_t)(g * 512 + piece * 16) : kOob);
@@ -336,7 +339,7 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_xwave_kernel(
     uint2 *xs2 = reinterpret_cast<uint2 *>(xslice);
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-        if (ks + i * SK < P) { /* wave-uniform */
+        if (gw + i * kStride < P) { /* wave-uniform */
             xs2[i * 64 + lane] = xv[i];
             /* lane l holds chunk c = l / 2 = 16 gl + 4 s + kb of the pair: add the chunk's two
              * halves (xor 1) and its four s (xor 8, 16); lane 32 gl + 2 kb then holds (gl, kb) */
@@ -352,34 +355,39 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_xwave_kernel(
         }
     }
 
-    /* 3. lanes r, r+8, ..., r+56 hold row r's partials; then the SK waves of a tile */
+    /* 3. lanes r, r+8, ..., r+56 hold row r's partials; then the SK waves of the block */
     acc += __shfl_xor(acc, 8);
     acc += __shfl_xor(acc, 16);
     acc += __shfl_xor(acc, 32);
-    float row_sum = acc;
-    if (SK > 1) {
-        if (lane < 8) red[wave * 8 + lane] = acc;
-        __syncthreads();
-        if (ks == 0 && lane < 8) {
-            row_sum = 0.0f;
+    if (lane < 8) red[wave * 8 + lane] = acc;
+    __syncthreads();
+    if (wave != 0 || lane >= 8) return;
+    float row_sum = 0.0f;
 #pragma unroll
-            for (int w = 0; w < SK; ++w) row_sum += red[(wave + w) * 8 + lane];
-        }
+    for (int w = 0; w < SK; ++w) row_sum += red[w * 8 + lane];
+
+    /* 4. the BS blocks of the tile */
+    if (BS > 1) {
+        float *pp = partial + (size_t)tile * BS * 8;
+        __hip_atomic_store(pp + part * 8 + lane, row_sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        unsigned prev = 0;
+        if (lane == 0)
+            prev = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+        prev = __shfl(prev, 0);
+        if (prev != BS - 1) return;
+        row_sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < BS; ++j)
+            row_sum += __hip_atomic_load(pp + j * 8 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0)
+            __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (ks != 0 || !tile_ok) return;
-    if (PAIR) {
-        const float upv = __shfl_down(row_sum, 4);
-        if (lane < 4) {
-            const float gate = bf16_widen(bf16_rne(row_sum));
-            const float up = bf16_widen(bf16_rne(upv));
-            reinterpret_cast<uint16_t *>(out)[tile * 4 + lane] = silu_mul_bf16(gate, up);
-        }
-    } else if (lane < 8) {
-        if (OUT_F32)
-            reinterpret_cast<float *>(out)[tile * 8 + lane] = row_sum;
-        else
-            reinterpret_cast<uint16_t *>(out)[tile * 8 + lane] = bf16_rne(row_sum);
-    }
+    if (OUT_F32)
+        reinterpret_cast<float *>(out)[tile * 8 + lane] = row_sum;
+    else
+        reinterpret_cast<uint16_t *>(out)[tile * 8 + lane] = bf16_rne(row_sum);
 }
 
 size_t xwave_smem(int waves, int np) { return (size_t)waves * np * 512 + (size_t)waves * 32; }
@@ -778,20 +786,27 @@ int launch_gemv_cfg(const uint16_t *x, const uint8_t *w, const uint16_t *s, void
     return hip_status(hipGetLastError(), "gemv launch");
 }
 
-template <bool OUT_F32, int NP>
+int split_scratch(size_t partial_bytes, size_t ncounters, float **partial, unsigned **counters);
+
+template <bool OUT_F32, int NP, int SK, int BS>
 int launch_xwave_np(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N,
                     int K, hipStream_t stream) {
-    constexpr int SK = kXwaveWaves;
-    hipLaunchKernelGGL((gemv_xwave_kernel<false, OUT_F32, 1, SK, NP>), dim3(N / 8), dim3(SK * 64),
-                       xwave_smem(SK, NP), stream, x, w, s, out, N, K);
+    float *partial = nullptr;
+    unsigned *counters = nullptr;
+    if (BS > 1) {
+        int st = split_scratch((size_t)(N / 8) * BS * 8 * sizeof(float), (size_t)(N / 8),
+                               &partial, &counters);
+        if (st) return st;
+    }
+    hipLaunchKernelGGL((gemv_xwave_kernel<OUT_F32, SK, NP, BS>), dim3(N / 8 * BS), dim3(SK * 64),
+                       xwave_smem(SK, NP), stream, x, w, s, out, N, K, partial, counters);
     return hip_status(hipGetLastError(), "gemv launch");
 }
 
 /* Block shapes (measured on MI355X, graph-replayed, weights rotated past the MALL):
  * - a long K (more group pairs than one wave holds, the down projection) runs the wave-local
- *   activation kernel with kXwaveWaves waves on one tile, NP = ceil(pairs / kXwaveWaves) each:
- *   at K = 9728 / 8704 / 17408 it takes 5.85 / 8.35 / 14.1 us against 6.2 / 9.7 / 15.7 us for the
- *   block-staged kernel;
+ *   activation kernel: at K = 9728 / 8704 / 17408 it takes 5.85 / 8.35 / 12.9 us against
+ *   6.2 / 9.7 / 15.7 us for the block-staged kernel;
  * - otherwise the block-staged kernel, split-K being the smallest power of two that keeps a
  *   wave at <= kMaxLoads pieces; a single-wave tile is split in two when it has more than six
  *   pairs (K = 2560 pair operand: 8.28 against 8.56 us). */
@@ -800,15 +815,19 @@ int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *ou
                 hipStream_t stream, const NormArgs *norm = nullptr) {
     const int pairs = (K / 128 + 1) / 2;
     if (!PAIR && !norm && pairs > kMaxLoads) {
+        /* up to 48 pairs: one block of 16 waves a tile; beyond, split the tile over BS blocks of
+         * 8 waves holding at most 3 pairs each (K = 17408: 12.9 against 13.7 us) */
         switch ((pairs + kXwaveWaves - 1) / kXwaveWaves) {
-            case 1: return launch_xwave_np<OUT_F32, 1>(x, w, s, out, N, K, stream);
-            case 2: return launch_xwave_np<OUT_F32, 2>(x, w, s, out, N, K, stream);
-            case 3: return launch_xwave_np<OUT_F32, 3>(x, w, s, out, N, K, stream);
-            case 4: return launch_xwave_np<OUT_F32, 4>(x, w, s, out, N, K, stream);
-            case 5: return launch_xwave_np<OUT_F32, 5>(x, w, s, out, N, K, stream);
-            case 6: return launch_xwave_np<OUT_F32, 6>(x, w, s, out, N, K, stream);
-            case 7: return launch_xwave_np<OUT_F32, 7>(x, w, s, out, N, K, stream);
-            default: break; /* beyond the LDS slices: block-staged below */
+            case 1: return launch_xwave_np<OUT_F32, 1, kXwaveWaves, 1>(x, w, s, out, N, K, stream);
+            case 2: return launch_xwave_np<OUT_F32, 2, kXwaveWaves, 1>(x, w, s, out, N, K, stream);
+            case 3: return launch_xwave_np<OUT_F32, 3, kXwaveWaves, 1>(x, w, s, out, N, K, stream);
+            default: break;
+        }
+        switch ((pairs + 23) / 24) {
+            case 3: return launch_xwave_np<OUT_F32, 3, 8, 3>(x, w, s, out, N, K, stream);
+            case 4: return launch_xwave_np<OUT_F32, 3, 8, 4>(x, w, s, out, N, K, stream);
+            case 5: return launch_xwave_np<OUT_F32, 3, 8, 5>(x, w, s, out, N, K, stream);
+            default: break; /* K > 30720 is refused by check_gemm_args */
         }
     }
     int sk = 1;
