@@ -325,3 +325,22 @@ extern "C" int engine_ffn_forward_norm_partial_f32(EngineHandle *eng, int layer,
     return ffn_forward_norm(eng, layer, residual, norm_w, norm_style, eps, out, true, tokens,
                             stream);
 }
+
+extern "C" int engine_ffn_forward_residual_norm(EngineHandle *eng, int layer, uint16_t *residual,
+                                                const uint16_t *sublayer, const uint16_t *norm_w,
+                                                int norm_style, float eps, uint16_t *out,
+                                                int tokens, void *stream) {
+    W4A16FfnOperands op;
+    int st = engine_ffn_operands(eng, layer, &op);
+    if (st) return st;
+    if (eng->cfg.tp_size > 1)
+        return set_error(W4A16_ERR_CONFIG, "engine_ffn_forward_residual_norm: tensor parallelism "
+                         "adds the residual after the cross-rank sum; use engine_ffn_forward_norm_partial_f32");
+    if (tokens < 0 || tokens > eng->cfg.max_tokens)
+        return set_error(W4A16_ERR_CONFIG, "engine_ffn_forward_residual_norm: %d tokens, this engine holds workspace for %d",
+                         tokens, eng->cfg.max_tokens);
+    return mlp_int4_residual_norm_bf16(residual, sublayer, norm_w, norm_style, eps,
+                                       op.gate_up_packed, op.gate_up_scales, op.down_packed,
+                                       op.down_scales, out, static_cast<uint16_t *>(eng->act_ws.ptr),
+                                       tokens, op.hidden, op.intermediate, stream);
+}

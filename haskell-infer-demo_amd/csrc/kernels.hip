@@ -79,6 +79,14 @@ __device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
     return bf16_rne(silu_f32(gate) * up);
 }
 
+/* Two packed BF16 sums, each BF16(f32(a) + f32(b)) (the residual update of reference
+ * csrc/kernels/gdn_norm.cu:121-129 and flashinfer_norm.cu:124-126). */
+__device__ __forceinline__ uint32_t bf16_add2(uint32_t a, uint32_t b) {
+    const float lo = bf16_widen((uint16_t)(a & 0xFFFFu)) + bf16_widen((uint16_t)(b & 0xFFFFu));
+    const float hi = bf16_widen((uint16_t)(a >> 16)) + bf16_widen((uint16_t)(b >> 16));
+    return (uint32_t)bf16_rne(lo) | ((uint32_t)bf16_rne(hi) << 16);
+}
+
 /* Raw buffer access: an offset past num_records reads 0 without a branch, which keeps every
  * load of a wave unconditional (a predicated global load is compiled as a branch plus a wait). */
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
@@ -107,7 +115,8 @@ template <bool PAIR, bool OUT_F32, int TB, int SK, bool NORM>
 __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ wt,
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K,
-    const uint16_t *__restrict__ norm_w, float norm_bias, float eps) {
+    const uint16_t *__restrict__ norm_w, float norm_bias, float eps,
+    const uint16_t *__restrict__ sub) {
     constexpr int W = TB * SK;
     /* the largest K this configuration is launched for: SK * kMaxLoads group pairs */
     constexpr int kMaxK = (256 * kMaxLoads * SK < kMaxGemvK) ? 256 * kMaxLoads * SK : kMaxGemvK;
@@ -140,12 +149,16 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
         xv[it] = buf_load16(xr, i < xchunks ? (uint32_t)i * 16 : kOob);
     }
     uint4 nv[NORM ? kXIters : 1];
+    uint4 sv[NORM ? kXIters : 1];
     if (NORM) {
         const __amdgpu_buffer_rsrc_t nr = make_rsrc(norm_w, (uint32_t)K * 2);
+        /* a null sublayer reads as zeros (an empty buffer descriptor) */
+        const __amdgpu_buffer_rsrc_t ur = make_rsrc(sub, sub ? (uint32_t)K * 2 : 0u);
 #pragma unroll
         for (int it = 0; it < kXIters; ++it) {
             const int i = it * W * 64 + tid;
             nv[it] = buf_load16(nr, i < xchunks ? (uint32_t)i * 16 : kOob);
+            sv[it] = buf_load16(ur, i < xchunks ? (uint32_t)i * 16 : kOob);
         }
     }
 
@@ -174,6 +187,17 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
         /* keep the weight loads above: without this fence the scheduler hoists the sum of
          * squares over them, and the weights would wait for the activation's round trip */
         __builtin_amdgcn_sched_barrier(0);
+        if (sub) { /* plan F2: the norm reads BF16(residual + sublayer) */
+#pragma unroll
+            for (int it = 0; it < kXIters; ++it) {
+                const uint32_t a4[4] = {xv[it].x, xv[it].y, xv[it].z, xv[it].w};
+                const uint32_t b4[4] = {sv[it].x, sv[it].y, sv[it].z, sv[it].w};
+                uint32_t o4[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) o4[q] = bf16_add2(a4[q], b4[q]);
+                xv[it] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+            }
+        }
         float ss = 0.0f;
 #pragma unroll
         for (int it = 0; it < kXIters; ++it) {
@@ -290,7 +314,7 @@ template <bool OUT_F32, int SK, int NP, int BS>
 __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ wt,
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, float *partial,
-    unsigned *counters) {
+    unsigned *counters, uint16_t *residual, const uint16_t *sub) {
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
     const int P = (G + 1) >> 1;
@@ -384,10 +408,20 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
         if (lane == 0)
             __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (OUT_F32)
+    if (OUT_F32) {
         reinterpret_cast<float *>(out)[tile * 8 + lane] = row_sum;
-    else
-        reinterpret_cast<uint16_t *>(out)[tile * 8 + lane] = bf16_rne(row_sum);
+    } else {
+        const int row = tile * 8 + lane;
+        const uint16_t o = bf16_rne(row_sum);
+        if (residual) {
+            /* plan F2 epilogue: residual <- BF16(BF16(residual + sub) + out), the updates of
+             * reference csrc/layer_dispatch.cu:193-209 (this row's inputs are read before
+             * its output is written, so sub may alias out) */
+            const uint16_t rsum = (uint16_t)(bf16_add2(residual[row], sub[row]) & 0xFFFFu);
+            residual[row] = (uint16_t)(bf16_add2(rsum, o) & 0xFFFFu);
+        }
+        reinterpret_cast<uint16_t *>(out)[row] = o;
+    }
 }
 
 size_t xwave_smem(int waves, int np) { return (size_t)waves * np * 512 + (size_t)waves * 32; }
@@ -611,19 +645,35 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
  * cols % 8 == 0 and cols <= CH * 8 * 256 (the launcher checks). */
 template <int CH>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t *__restrict__ out,
-                                                      const uint16_t *__restrict__ x,
+                                                      uint16_t *x,
                                                       const uint16_t *__restrict__ w, int cols,
-                                                      float bias, float eps) {
+                                                      float bias, float eps,
+                                                      const uint16_t *sub) {
     __shared__ float red[4];
     const int chunks = cols >> 3;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + (size_t)blockIdx.x * cols, (uint32_t)cols * 2);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(w, (uint32_t)cols * 2);
-    uint4 xv[CH], wv[CH];
+    const __amdgpu_buffer_rsrc_t ur =
+        make_rsrc(sub ? sub + (size_t)blockIdx.x * cols : sub, sub ? (uint32_t)cols * 2 : 0u);
+    uint4 xv[CH], wv[CH], uv[CH];
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int i = c * 256 + threadIdx.x;
         xv[c] = buf_load16(xr, i < chunks ? (uint32_t)i * 16 : kOob);
         wv[c] = buf_load16(wr, i < chunks ? (uint32_t)i * 16 : kOob);
+        uv[c] = buf_load16(ur, i < chunks ? (uint32_t)i * 16 : kOob);
+    }
+    if (sub) {
+        /* plan F2 (reference csrc/kernels/flashinfer_norm.cu:111-155): the residual becomes
+         * BF16(x + sub), is stored back, and the norm reads the rounded value */
+        uint4 *xrow = reinterpret_cast<uint4 *>(x + (size_t)blockIdx.x * cols);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int i = c * 256 + threadIdx.x;
+            xv[c] = make_uint4(bf16_add2(xv[c].x, uv[c].x), bf16_add2(xv[c].y, uv[c].y),
+                               bf16_add2(xv[c].z, uv[c].z), bf16_add2(xv[c].w, uv[c].w));
+            if (i < chunks) xrow[i] = xv[c];
+        }
     }
     float ss = 0.0f;
 #pragma unroll
@@ -661,6 +711,18 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t *__restrict__ out
         }
         if (i < chunks) orow[i] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
     }
+}
+
+/* dst <- BF16(dst + src), 8 elements a thread (reference csrc/kernels/gdn_norm.cu:121-129). */
+__global__ __launch_bounds__(256) void residual_add_kernel(uint16_t *__restrict__ dst,
+                                                           const uint16_t *__restrict__ src,
+                                                           long long chunks) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= chunks) return;
+    uint4 *d = reinterpret_cast<uint4 *>(dst) + i;
+    const uint4 a = *d, b = reinterpret_cast<const uint4 *>(src)[i];
+    *d = make_uint4(bf16_add2(a.x, b.x), bf16_add2(a.y, b.y), bf16_add2(a.z, b.z),
+                    bf16_add2(a.w, b.w));
 }
 
 __global__ void silu_mul_packed_kernel(uint16_t *__restrict__ out,
@@ -769,6 +831,7 @@ size_t gemv_smem(int K, int waves) {
 struct NormArgs {
     const uint16_t *w = nullptr;
     float bias = 0.0f, eps = 0.0f;
+    const uint16_t *sub = nullptr; /* plan F2: normalise BF16(x + sub) */
 };
 
 template <bool PAIR, bool OUT_F32, int TB, int SK>
@@ -778,11 +841,11 @@ int launch_gemv_cfg(const uint16_t *x, const uint8_t *w, const uint16_t *s, void
     if (norm)
         hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK, true>),
                            dim3((tiles + TB - 1) / TB), dim3(TB * SK * 64), gemv_smem(K, TB * SK),
-                           stream, x, w, s, out, N, K, norm->w, norm->bias, norm->eps);
+                           stream, x, w, s, out, N, K, norm->w, norm->bias, norm->eps, norm->sub);
     else
         hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK, false>),
                            dim3((tiles + TB - 1) / TB), dim3(TB * SK * 64), gemv_smem(K, TB * SK),
-                           stream, x, w, s, out, N, K, nullptr, 0.0f, 0.0f);
+                           stream, x, w, s, out, N, K, nullptr, 0.0f, 0.0f, nullptr);
     return hip_status(hipGetLastError(), "gemv launch");
 }
 
@@ -790,7 +853,8 @@ int split_scratch(size_t partial_bytes, size_t ncounters, float **partial, unsig
 
 template <bool OUT_F32, int NP, int SK, int BS>
 int launch_xwave_np(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N,
-                    int K, hipStream_t stream) {
+                    int K, hipStream_t stream, uint16_t *residual = nullptr,
+                    const uint16_t *sub = nullptr) {
     float *partial = nullptr;
     unsigned *counters = nullptr;
     if (BS > 1) {
@@ -799,8 +863,31 @@ int launch_xwave_np(const uint16_t *x, const uint8_t *w, const uint16_t *s, void
         if (st) return st;
     }
     hipLaunchKernelGGL((gemv_xwave_kernel<OUT_F32, SK, NP, BS>), dim3(N / 8 * BS), dim3(SK * 64),
-                       xwave_smem(SK, NP), stream, x, w, s, out, N, K, partial, counters);
+                       xwave_smem(SK, NP), stream, x, w, s, out, N, K, partial, counters, residual,
+                       sub);
     return hip_status(hipGetLastError(), "gemv launch");
+}
+
+/* The wave-local kernel for a K of more than kMaxLoads group pairs: up to 48 pairs one block of
+ * 16 waves a tile; beyond, the tile split over BS blocks of 8 waves holding at most 3 pairs each
+ * (K = 17408: 12.9 against 13.7 us). residual / sub: the plan-F2 epilogue (BF16 output only).
+ * Returns 1 when K is beyond its shapes. */
+template <bool OUT_F32>
+int launch_xwave(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N, int K,
+                 hipStream_t stream, uint16_t *residual = nullptr, const uint16_t *sub = nullptr) {
+    const int pairs = (K / 128 + 1) / 2;
+    switch ((pairs + kXwaveWaves - 1) / kXwaveWaves) {
+        case 1: return launch_xwave_np<OUT_F32, 1, kXwaveWaves, 1>(x, w, s, out, N, K, stream, residual, sub);
+        case 2: return launch_xwave_np<OUT_F32, 2, kXwaveWaves, 1>(x, w, s, out, N, K, stream, residual, sub);
+        case 3: return launch_xwave_np<OUT_F32, 3, kXwaveWaves, 1>(x, w, s, out, N, K, stream, residual, sub);
+        default: break;
+    }
+    switch ((pairs + 23) / 24) {
+        case 3: return launch_xwave_np<OUT_F32, 3, 8, 3>(x, w, s, out, N, K, stream, residual, sub);
+        case 4: return launch_xwave_np<OUT_F32, 3, 8, 4>(x, w, s, out, N, K, stream, residual, sub);
+        case 5: return launch_xwave_np<OUT_F32, 3, 8, 5>(x, w, s, out, N, K, stream, residual, sub);
+        default: return 1;
+    }
 }
 
 /* Block shapes (measured on MI355X, graph-replayed, weights rotated past the MALL):
@@ -815,20 +902,8 @@ int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *ou
                 hipStream_t stream, const NormArgs *norm = nullptr) {
     const int pairs = (K / 128 + 1) / 2;
     if (!PAIR && !norm && pairs > kMaxLoads) {
-        /* up to 48 pairs: one block of 16 waves a tile; beyond, split the tile over BS blocks of
-         * 8 waves holding at most 3 pairs each (K = 17408: 12.9 against 13.7 us) */
-        switch ((pairs + kXwaveWaves - 1) / kXwaveWaves) {
-            case 1: return launch_xwave_np<OUT_F32, 1, kXwaveWaves, 1>(x, w, s, out, N, K, stream);
-            case 2: return launch_xwave_np<OUT_F32, 2, kXwaveWaves, 1>(x, w, s, out, N, K, stream);
-            case 3: return launch_xwave_np<OUT_F32, 3, kXwaveWaves, 1>(x, w, s, out, N, K, stream);
-            default: break;
-        }
-        switch ((pairs + 23) / 24) {
-            case 3: return launch_xwave_np<OUT_F32, 3, 8, 3>(x, w, s, out, N, K, stream);
-            case 4: return launch_xwave_np<OUT_F32, 3, 8, 4>(x, w, s, out, N, K, stream);
-            case 5: return launch_xwave_np<OUT_F32, 3, 8, 5>(x, w, s, out, N, K, stream);
-            default: break; /* K > 30720 is refused by check_gemm_args */
-        }
+        const int st = launch_xwave<OUT_F32>(x, w, s, out, N, K, stream);
+        if (st <= 0) return st;
     }
     int sk = 1;
     while (sk < 16 && (pairs + sk - 1) / sk > kMaxLoads) sk *= 2;
@@ -1074,15 +1149,15 @@ static int norm_args(const uint16_t *w, int style, float eps, int cols, int rows
 }
 
 static int launch_rmsnorm(uint16_t *out, const uint16_t *x, const uint16_t *w, int cols, int rows,
-                          float bias, float eps, hipStream_t s) {
+                          float bias, float eps, hipStream_t s, const uint16_t *sub = nullptr) {
     const int ch = (cols / 8 + 255) / 256;
     if (cols % 8 || ch > 8)
         return set_error(W4A16_ERR_CONFIG, "rmsnorm: cols=%d must be a multiple of 8 and <= 16384",
                          cols);
-    if (ch <= 1) hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(rows), dim3(256), 0, s, out, x, w, cols, bias, eps);
-    else if (ch <= 2) hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3(rows), dim3(256), 0, s, out, x, w, cols, bias, eps);
-    else if (ch <= 4) hipLaunchKernelGGL(rmsnorm_kernel<4>, dim3(rows), dim3(256), 0, s, out, x, w, cols, bias, eps);
-    else hipLaunchKernelGGL(rmsnorm_kernel<8>, dim3(rows), dim3(256), 0, s, out, x, w, cols, bias, eps);
+    if (ch <= 1) hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(rows), dim3(256), 0, s, out, const_cast<uint16_t *>(x), w, cols, bias, eps, sub);
+    else if (ch <= 2) hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3(rows), dim3(256), 0, s, out, const_cast<uint16_t *>(x), w, cols, bias, eps, sub);
+    else if (ch <= 4) hipLaunchKernelGGL(rmsnorm_kernel<4>, dim3(rows), dim3(256), 0, s, out, const_cast<uint16_t *>(x), w, cols, bias, eps, sub);
+    else hipLaunchKernelGGL(rmsnorm_kernel<8>, dim3(rows), dim3(256), 0, s, out, const_cast<uint16_t *>(x), w, cols, bias, eps, sub);
     return hip_status(hipGetLastError(), "rmsnorm launch");
 }
 
@@ -1138,6 +1213,62 @@ extern "C" int mlp_int4_norm_bf16(const uint16_t *residual, const uint16_t *norm
                                   void *stream) {
     return mlp_norm_common(residual, norm_w, norm_style, eps, gup, gus, dnp, dns, out, false, ws,
                            M, hidden, inter, stream);
+}
+
+/* Plan F2 around the INT4 MLP (reference csrc/layer_dispatch.cu:183-209): residual <-
+ * BF16(residual + sublayer); normed = RMSNorm(residual); out = MLP(normed); residual <-
+ * BF16(residual + out). At M = 1 with a one-wave gate/up tile and a wave-local down kernel the
+ * whole sequence is two launches: the gate/up kernel normalises BF16(residual + sublayer) in its
+ * staging (writing nothing back, since every block reads the residual), and the down kernel's
+ * epilogue forms both residual updates for its rows. Otherwise a norm kernel stores the first
+ * update, and an add kernel the second. sublayer may alias out (as in the reference, where the
+ * mixer output and the layer output share a buffer). */
+extern "C" int mlp_int4_residual_norm_bf16(uint16_t *residual, const uint16_t *sublayer,
+                                           const uint16_t *norm_w, int norm_style, float eps,
+                                           const uint8_t *gup, const uint16_t *gus,
+                                           const uint8_t *dnp, const uint16_t *dns, uint16_t *out,
+                                           uint16_t *ws, int M, int hidden, int inter,
+                                           void *stream) {
+    if (M < 0 || hidden <= 0 || inter <= 0)
+        return set_error(W4A16_ERR_CONFIG, "mlp_int4_residual_norm: bad extents M=%d hidden=%d inter=%d",
+                         M, hidden, inter);
+    NormArgs na;
+    int st = norm_args(norm_w, norm_style, eps, hidden, M, &na, "mlp_int4_residual_norm");
+    if (st) return st;
+    if (M == 0) return W4A16_OK;
+    if (!residual || !sublayer || !ws || !out)
+        return set_error(W4A16_ERR_CONFIG, "mlp_int4_residual_norm: null buffer");
+    if (hidden % 8)
+        return set_error(W4A16_ERR_CONFIG, "mlp_int4_residual_norm: hidden=%d is not a multiple of 8",
+                         hidden);
+    st = check_gemm_args(residual, gup, gus, ws, M, 2 * inter, hidden, W4A16_GROUP,
+                         "mlp_int4_residual_norm gate/up");
+    if (st < 0) return st;
+    st = check_gemm_args(ws, dnp, dns, out, M, hidden, inter, W4A16_GROUP,
+                         "mlp_int4_residual_norm down");
+    if (st < 0) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint16_t *normed = ws;
+    uint16_t *act = ws + (size_t)M * hidden;
+    const int gu_pairs = (hidden / W4A16_GROUP + 1) / 2;
+    const int dn_pairs = (inter / W4A16_GROUP + 1) / 2;
+    if (M == 1 && gu_pairs <= kMaxLoads && dn_pairs > kMaxLoads) {
+        na.sub = sublayer;
+        st = launch_gemv<true, false>(residual, gup, gus, act, 2 * inter, hidden, s, &na);
+        if (st) return st;
+        st = launch_xwave<false>(act, dnp, dns, out, hidden, inter, s, residual, sublayer);
+        if (st <= 0) return st;
+        return set_error(W4A16_ERR_CONFIG, "mlp_int4_residual_norm: K=%d beyond the down kernels",
+                         inter);
+    }
+    st = launch_rmsnorm(normed, residual, norm_w, hidden, M, na.bias, eps, s, sublayer);
+    if (!st) st = run_rows<kOutPairSilu>(normed, M, gup, gus, act, 2 * inter, hidden, s);
+    if (!st) st = run_rows<kOutBf16>(act, M, dnp, dns, out, hidden, inter, s);
+    if (st) return st;
+    const long long chunks = (long long)M * hidden / 8;
+    hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, s,
+                       residual, out, chunks);
+    return hip_status(hipGetLastError(), "residual add launch");
 }
 
 extern "C" int mlp_int4_norm_partial_f32(const uint16_t *residual, const uint16_t *norm_w,

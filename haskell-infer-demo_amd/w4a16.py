@@ -67,6 +67,10 @@ _SIGNATURES = {
                                 _i, _vp]),
     "mlp_int4_norm_partial_f32": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp,
                                        _i, _i, _i, _vp]),
+    "mlp_int4_residual_norm_bf16": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _vp,
+                                         _vp, _vp, _i, _i, _i, _vp]),
+    "engine_ffn_forward_residual_norm": (_i, [_vp, _i, _vp, _vp, _vp, _i, ctypes.c_float, _vp, _i,
+                                              _vp]),
     "mlp_int4_partial_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "w4a16_manifest_check": (_i, [ctypes.c_char_p, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "w4a16_artifact_verify": (_i, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _ll,
@@ -349,6 +353,26 @@ def mlp_int4_norm(residual, norm_w, norm_style, eps, gu, dn, out=None, ws=None, 
     return out
 
 
+def mlp_int4_residual_norm(residual, sublayer, norm_w, norm_style, eps, gu, dn, out=None, ws=None,
+                           stream=None):
+    """Plan F2: residual <- BF16(residual + sublayer); out = MLP(RMSNorm(residual));
+    residual <- BF16(residual + out). residual is updated in place; returns out."""
+    import torch
+
+    m, h = residual.shape
+    inter = gu.n // 2
+    if ws is None:
+        ws = torch.empty((m, h + inter), dtype=residual.dtype, device=residual.device)
+    if out is None:
+        out = torch.empty((m, h), dtype=residual.dtype, device=residual.device)
+    _check(lib.mlp_int4_residual_norm_bf16(residual.data_ptr(), sublayer.data_ptr(),
+                                           norm_w.data_ptr(), norm_style, eps, gu.packed.data_ptr(),
+                                           gu.scales.data_ptr(), dn.packed.data_ptr(),
+                                           dn.scales.data_ptr(), out.data_ptr(), ws.data_ptr(), m, h,
+                                           inter, _stream(stream)), "mlp_int4_residual_norm")
+    return out
+
+
 # ----------------------------------------------------------------------------------------------
 # Sidecar and the operand store (engine_load_quantized_ffn)
 # ----------------------------------------------------------------------------------------------
@@ -455,4 +479,19 @@ class Engine:
               else lib.engine_ffn_forward_norm)
         _check(fn(self.handle, layer, residual.data_ptr(), norm_w.data_ptr(), norm_style, eps,
                   out.data_ptr(), m, _stream(stream)), "engine_ffn_forward_norm")
+        return out
+
+    def forward_residual_norm(self, layer, residual, sublayer, norm_w, norm_style, eps, out=None,
+                              stream=None):
+        """Plan F2 (tp = 1): updates residual in place and returns the layer output."""
+        import torch
+
+        m = residual.shape[0]
+        if out is None:
+            out = torch.empty((m, self.hidden), dtype=residual.dtype, device=residual.device)
+        _check(lib.engine_ffn_forward_residual_norm(self.handle, layer, residual.data_ptr(),
+                                                    sublayer.data_ptr(), norm_w.data_ptr(),
+                                                    norm_style, eps, out.data_ptr(), m,
+                                                    _stream(stream)),
+               "engine_ffn_forward_residual_norm")
         return out

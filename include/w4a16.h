@@ -150,6 +150,21 @@ int mlp_int4_norm_bf16(const uint16_t *residual, const uint16_t *norm_w, int nor
                        const uint8_t *dn_packed, const uint16_t *dn_scales, uint16_t *out,
                        uint16_t *ws, int M, int hidden, int intermediate, void *stream);
 
+/* Plan F2 around the INT4 MLP (reference csrc/layer_dispatch.cu:183-209 with
+ * kernel_residual_norm, csrc/kernels/flashinfer_norm.cu:111-175, and kernel_residual_add,
+ * csrc/kernels/gdn_norm.cu:121-136), for a dense layer without tensor parallelism:
+ *   residual <- BF16(residual + sublayer); out = MLP(RMSNorm(residual));
+ *   residual <- BF16(residual + out).
+ * residual [M, hidden] is updated in place; sublayer may alias out. ws as mlp_int4_norm_bf16.
+ * At M = 1 this is two launches (the norm in the gate/up staging, both residual updates in the
+ * down projection's epilogue). */
+int mlp_int4_residual_norm_bf16(uint16_t *residual, const uint16_t *sublayer,
+                                const uint16_t *norm_w, int norm_style, float eps,
+                                const uint8_t *gu_packed, const uint16_t *gu_scales,
+                                const uint8_t *dn_packed, const uint16_t *dn_scales,
+                                uint16_t *out, uint16_t *ws, int M, int hidden, int intermediate,
+                                void *stream);
+
 /* Same, with the tensor-parallel FP32 partial of the down projection (as mlp_int4_partial_f32). */
 int mlp_int4_norm_partial_f32(const uint16_t *residual, const uint16_t *norm_w, int norm_style,
                               float eps, const uint8_t *gu_packed, const uint16_t *gu_scales,
@@ -251,6 +266,13 @@ int engine_ffn_forward_norm(EngineHandle *engine, int layer, const uint16_t *res
 int engine_ffn_forward_norm_partial_f32(EngineHandle *engine, int layer, const uint16_t *residual,
                                         const uint16_t *norm_w, int norm_style, float eps,
                                         float *out, int tokens, void *stream);
+
+/* Plan F2 on a loaded layer (see mlp_int4_residual_norm_bf16); refused under tensor parallelism,
+ * where the residual add follows the cross-rank sum (reference csrc/layer_dispatch.cu:166-169). */
+int engine_ffn_forward_residual_norm(EngineHandle *engine, int layer, uint16_t *residual,
+                                     const uint16_t *sublayer, const uint16_t *norm_w,
+                                     int norm_style, float eps, uint16_t *out, int tokens,
+                                     void *stream);
 
 /* ---------------------------------------------------------------------------------------
  * Test bridges (host pointers, artifact layout; synchronous).

@@ -44,6 +44,9 @@ def _load():
         "orc_ffn_bf16": (ctypes.c_int, [_ll, _ll, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
         "orc_ffn_partial_f32": (ctypes.c_int, [_ll, _ll, _ll, _vp, _vp, _vp, _vp, _vp, _vp]),
         "orc_rmsnorm_bf16": (ctypes.c_int, [_ll, _ll, _vp, _vp, ctypes.c_int, ctypes.c_double, _vp]),
+        "orc_residual_norm_bf16": (ctypes.c_int, [_ll, _ll, _vp, _vp, _vp, ctypes.c_int,
+                                                  ctypes.c_double, _vp]),
+        "orc_residual_add_bf16": (ctypes.c_int, [_ll, _vp, _vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -166,6 +169,24 @@ def rmsnorm_bf16(x_bits, w_bits, norm_style, eps):
     _ok(lib.orc_rmsnorm_bf16(rows, cols, _p(x), _p(_c(w_bits, np.uint16)), norm_style, eps,
                              _p(out)), "rmsnorm_bf16")
     return out
+
+
+def residual_norm_bf16(residual_bits, sub_bits, w_bits, norm_style, eps):
+    """Returns (updated residual, normed) as BF16 bits [rows, cols]; the input is not modified."""
+    r = np.array(_c(residual_bits, np.uint16), copy=True)
+    r = r.reshape(1, -1) if r.ndim == 1 else r
+    rows, cols = r.shape
+    out = np.zeros((rows, cols), np.uint16)
+    _ok(lib.orc_residual_norm_bf16(rows, cols, _p(r), _p(_c(sub_bits, np.uint16)),
+                                   _p(_c(w_bits, np.uint16)), norm_style, eps, _p(out)),
+        "residual_norm_bf16")
+    return r, out
+
+
+def residual_add_bf16(dst_bits, src_bits):
+    d = np.array(_c(dst_bits, np.uint16), copy=True)
+    _ok(lib.orc_residual_add_bf16(d.size, _p(d), _p(_c(src_bits, np.uint16))), "residual_add_bf16")
+    return d
 
 
 def lib_rmsnorm_raw(cols, eps, norm_style, rows=1):

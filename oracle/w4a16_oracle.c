@@ -274,3 +274,25 @@ int orc_rmsnorm_bf16(long long rows, long long cols, const uint16_t *x, const ui
     }
     return ORC_OK;
 }
+
+/* reference csrc/kernels/gdn_norm.cu:121-129. */
+int orc_residual_add_bf16(long long n, uint16_t *dst, const uint16_t *src) {
+    if (n < 0) return fail(ORC_ERR_RANGE, "negative extent");
+    if (n > 0 && (!dst || !src)) return fail(ORC_ERR_ARG, "null argument");
+    for (long long i = 0; i < n; ++i)
+        dst[i] = orc_f32_to_bf16(orc_bf16_to_f32(dst[i]) + orc_bf16_to_f32(src[i]));
+    return ORC_OK;
+}
+
+/* reference csrc/kernels/flashinfer_norm.cu:111-175 (residual_norm_kernel and its wrapper). */
+int orc_residual_norm_bf16(long long rows, long long cols, uint16_t *residual,
+                           const uint16_t *sub, const uint16_t *w, int norm_style, double eps,
+                           uint16_t *out) {
+    if (rows < 0 || cols <= 0 || !isfinite(eps) || eps <= 0.0)
+        return fail(ORC_ERR_RANGE, "invalid shape or epsilon");
+    if (rows == 0) return ORC_OK;
+    if (!residual || !sub || !w || !out) return fail(ORC_ERR_ARG, "null argument");
+    int st = orc_residual_add_bf16(rows * cols, residual, sub);
+    if (st) return st;
+    return orc_rmsnorm_bf16(rows, cols, residual, w, norm_style, eps, out);
+}

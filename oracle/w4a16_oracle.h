@@ -102,6 +102,17 @@ int orc_ffn_partial_f32(long long m, long long hidden, long long inter, const ui
 int orc_rmsnorm_bf16(long long rows, long long cols, const uint16_t *x_bf16,
                      const uint16_t *w_bf16, int norm_style, double eps, uint16_t *out_bf16);
 
+/* Plan F2's fused residual update and norm (reference csrc/kernels/flashinfer_norm.cu:111-155,
+ * in-tree): residual[r, c] <- BF16(residual + sublayer) (stored back), then out = the RMSNorm of
+ * the rounded residual, as orc_rmsnorm_bf16 (the reference kernel's FP32 order is the same:
+ * value * scale * weight, weight + 1 for Gemma). */
+int orc_residual_norm_bf16(long long rows, long long cols, uint16_t *residual,
+                           const uint16_t *sublayer, const uint16_t *w_bf16, int norm_style,
+                           double eps, uint16_t *out_bf16);
+
+/* dst[i] <- BF16(f32(dst[i]) + f32(src[i])) (reference csrc/kernels/gdn_norm.cu:121-129). */
+int orc_residual_add_bf16(long long n, uint16_t *dst, const uint16_t *src);
+
 #ifdef __cplusplus
 }
 #endif

@@ -87,6 +87,18 @@ def test_load_and_forward_tp1(cuda, model):
         ref, _, _ = oracle.ffn_bf16(normed, gup, gus, dp, ds, H, I)
         assert_parity(got.cpu().numpy().view(np.uint16), ref, f"engine norm layer {layer}",
                       floor_div=16.0)
+        # plan F2: residual update, norm, FFN, residual add
+        print(f"engine tp=1 forward_residual_norm layer {layer}", flush=True)
+        sub = oracle.synth_activation(1, H, 30 + layer)
+        res = xd.clone()
+        got = eng.forward_residual_norm(layer, res, torch.from_numpy(sub.view(np.int16)).to(cuda),
+                                        torch.from_numpy(nw.view(np.int16)).to(cuda), 1, 1e-6)
+        r_mid, normed = oracle.residual_norm_bf16(x, sub, nw, 1, 1e-6)
+        ref, _, _ = oracle.ffn_bf16(normed, gup, gus, dp, ds, H, I)
+        assert_parity(got.cpu().numpy().view(np.uint16), ref, f"engine F2 layer {layer}",
+                      floor_div=16.0)
+        assert_parity(res.cpu().numpy().view(np.uint16), oracle.residual_add_bf16(r_mid, ref),
+                      f"engine F2 residual layer {layer}", floor_div=16.0)
     eng.close()
 
 
@@ -117,6 +129,8 @@ def test_load_and_forward_tp2(cuda, model):
                               oracle.dequantize_numpy(sdp, sds, H, li).view(np.uint32))
         print(f"engine tp=2 rank {rank} forward", flush=True)
         part = eng.forward(0, xd, partial_f32=True).cpu().numpy()
+        with pytest.raises(w4a16.W4A16Error):  # F2 adds the residual after the cross-rank sum
+            eng.forward_residual_norm(0, xd.clone(), xd, xd[0], 1, 1e-6)
         want = oracle.ffn_partial_f32(x, sgp, sgs, sdp, sds, H, li)
         rel = np.linalg.norm(part.astype(np.float64) - want) / np.linalg.norm(want)
         assert rel <= 1e-3, rel

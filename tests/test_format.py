@@ -143,3 +143,21 @@ def test_norm_entry_refusals_without_touching_the_device():
         w4a16.W4A16_ERR_CONFIG
     assert lib.mlp_int4_norm_bf16(dummy, dummy, 1, 1e-6, *args, 0, 2560, 9728, None) == \
         w4a16.W4A16_OK
+
+
+def test_residual_norm_entry_refusals_without_touching_the_device():
+    """mlp_int4_residual_norm_bf16 (plan F2) refuses before any device call: bad extents, a bad
+    epsilon or style, null buffers, hidden not a multiple of 8; M == 0 is a no-op."""
+    lib = w4a16.lib
+    d = 16
+    w = (d, d, d, d)
+    assert lib.mlp_int4_residual_norm_bf16(d, d, d, 1, 0.0, *w, d, d, 1, 2560, 9728, None) == \
+        w4a16.W4A16_ERR_CONFIG
+    assert lib.mlp_int4_residual_norm_bf16(d, d, d, 5, 1e-6, *w, d, d, 1, 2560, 9728, None) == \
+        w4a16.W4A16_ERR_CONFIG
+    assert lib.mlp_int4_residual_norm_bf16(d, None, d, 1, 1e-6, *w, d, d, 1, 2560, 9728, None) == \
+        w4a16.W4A16_ERR_CONFIG
+    assert lib.mlp_int4_residual_norm_bf16(d, d, d, 1, 1e-6, *w, d, d, -1, 2560, 9728, None) == \
+        w4a16.W4A16_ERR_CONFIG
+    assert lib.mlp_int4_residual_norm_bf16(d, d, d, 1, 1e-6, *w, d, d, 0, 2560, 9728, None) == \
+        w4a16.W4A16_OK

@@ -266,6 +266,41 @@ def test_ffn_norm_parity(cuda, style, m):
     assert rel <= 1e-3, rel
 
 
+@pytest.mark.parametrize("style", [0, 1])
+@pytest.mark.parametrize("m", [1, 2, 16])
+def test_ffn_residual_norm_parity(cuda, style, m):
+    """Plan F2 around the MLP (reference csrc/layer_dispatch.cu:183-209): the layer output
+    against the oracle (residual update, norm, FFN) at the end-to-end bar, and the updated
+    residual BF16(BF16(r + s) + out) bit-exact given the kernel's own output; at M = 1 also with
+    the sublayer aliasing the output buffer, as the reference's layer_out does."""
+    import torch
+
+    hidden, inter = 2560, 9728
+    say(f"ffn residual norm style={style} M={m}")
+    gup, gus, dp, ds = make_ffn(hidden, inter)
+    x, w = norm_inputs(m, hidden, style, seed=80 + m)
+    sub = oracle.bf16_bits(oracle.bf16_to_f32(oracle.synth_activation(m, hidden, seed=90 + m)) *
+                           np.float32(0.5))
+    gu = w4a16.TiledWeight.from_artifact(gup, gus, 2 * inter, hidden, pair=True, device=cuda)
+    dn = w4a16.TiledWeight.from_artifact(dp, ds, hidden, inter, device=cuda)
+    r_mid, normed = oracle.residual_norm_bf16(x, sub, w, style, 1e-6)
+    ref, _, _ = oracle.ffn_bf16(normed, gup, gus, dp, ds, hidden, inter)
+    r_ref = oracle.residual_add_bf16(r_mid, ref)
+    for alias in ((False, True) if m == 1 else (False,)):
+        res = to_dev(x, cuda)
+        sd = to_dev(sub, cuda)
+        out = sd if alias else torch.empty_like(sd)
+        got = from_dev(w4a16.mlp_int4_residual_norm(res, sd, to_dev(w, cuda), style, 1e-6, gu, dn,
+                                                    out=out))
+        assert_parity(got, ref, f"F2 out M={m} alias={alias}", floor_div=16.0)
+        # the residual is exact arithmetic on exact inputs: BF16(BF16(r + s) + out) with the
+        # kernel's own out must match bit for bit (against the oracle's out it moves by the
+        # output's ULPs, which on a cancelling element are many of the residual's)
+        assert np.array_equal(from_dev(res), oracle.residual_add_bf16(r_mid, got)), (m, alias)
+        assert_parity(from_dev(res), r_ref, f"F2 residual M={m} alias={alias}", floor_div=16.0,
+                      max_ulp=16.0)
+
+
 def test_ffn_tp_slice_partial_f32(cuda):
     """Config 4: rank 0 of tp=2 on the 27B FFN, scales kept global (reference
     csrc/engine.cu:2308-2369: gate/up rows 0..I/2-1 of each half, down columns 0..I/2-1)."""

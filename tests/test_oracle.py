@@ -290,3 +290,34 @@ def test_rmsnorm_closed_forms():
         c_, eps, style = bad
         with pytest.raises(oracle.OracleError):
             oracle.lib_rmsnorm_raw(c_, eps, style)
+
+
+def test_residual_norm_and_add_closed_forms():
+    """Plan F2's residual update and norm (reference csrc/kernels/flashinfer_norm.cu:111-155) and
+    the residual add (csrc/kernels/gdn_norm.cu:121-129):
+
+    * the add rounds f32(a) + f32(b) to nearest-even BF16: 1 + 2^-8 -> 1 (tie, even), 1 + 3 * 2^-8
+      -> 1 + 2^-6 (tie, even), 1 + 2^-8 + 2^-14 -> 1 + 2^-7 (past the tie), 2^-9 + 2^-9 exact;
+    * a zero sublayer leaves the residual unchanged and normalises exactly as orc_rmsnorm_bf16;
+    * sublayer = -residual zeroes both;
+    * the norm reads the rounded sum: residual = sublayer = the same row gives the RMSNorm of
+      2 x (a power of two, so rounding-free) = the RMSNorm of x.
+    """
+    b = oracle.bf16_bits(np.float32([1.0, 1.0, 1.0, 2.0 ** -9]))
+    d = oracle.bf16_bits(np.float32([2.0 ** -8, 3 * 2.0 ** -8, 2.0 ** -8 + 2.0 ** -14, 2.0 ** -9]))
+    got = oracle.bf16_to_f32(oracle.residual_add_bf16(b, d))
+    assert list(got) == [1.0, 1.0 + 2.0 ** -6, 1.0 + 2.0 ** -7, 2.0 ** -8]
+    cols = 512
+    rng = np.random.default_rng(12)
+    x = oracle.synth_activation(2, cols, seed=21)
+    w = oracle.bf16_bits(rng.normal(0.0, 0.3, cols).astype(np.float32))
+    for style in (0, 1):
+        r, n = oracle.residual_norm_bf16(x, np.zeros_like(x), w, style, 1e-6)
+        assert np.array_equal(r, x)
+        assert np.array_equal(n, oracle.rmsnorm_bf16(x, w, style, 1e-6))
+        neg = x ^ np.uint16(0x8000)
+        r, n = oracle.residual_norm_bf16(x, neg, w, style, 1e-6)
+        assert not np.any(r & 0x7FFF) and not np.any(n & 0x7FFF)
+        r, n = oracle.residual_norm_bf16(x, x, w, style, 1e-20)
+        assert np.array_equal(r, oracle.bf16_bits(2 * oracle.bf16_to_f32(x)))
+        assert np.array_equal(n, oracle.rmsnorm_bf16(x, w, style, 1e-20))
