@@ -27,7 +27,7 @@ namespace {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kMaxLoads = 12;     /* 16-byte pieces in flight per lane (all of a wave's share) */
+constexpr int kMaxLoads = 12;     /* group pairs one wave holds when it takes a whole tile (norm prologue) */
 constexpr int kMaxGemvK = 30464;  /* activation staged in LDS: 2K bytes + sums within 64 KiB */
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
@@ -110,16 +110,17 @@ constexpr uint32_t kOob = 0x80000000u; /* an offset no buffer here reaches: read
  * The activation loads are issued first, then every weight and scale load of the wave, so one
  * wait covers the activation and the weights stream while it is staged into LDS.
  * PAIR: a tile is 4 gate + 4 up rows and yields four BF16(silu(BF16 gate) x BF16 up) values;
- * otherwise eight BF16 outputs (or FP32 if OUT_F32). */
-template <bool PAIR, bool OUT_F32, int TB, int SK, bool NORM>
+ * otherwise eight BF16 outputs (or FP32 if OUT_F32). NL: the loads (group pairs) a wave holds,
+ * SK * NL >= pairs; sizing it to the shape keeps the VGPR count low enough for 8 waves a SIMD. */
+template <bool PAIR, bool OUT_F32, int TB, int SK, bool NORM, int NL>
 __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ wt,
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K,
     const uint16_t *__restrict__ norm_w, float norm_bias, float eps,
     const uint16_t *__restrict__ sub) {
     constexpr int W = TB * SK;
-    /* the largest K this configuration is launched for: SK * kMaxLoads group pairs */
-    constexpr int kMaxK = (256 * kMaxLoads * SK < kMaxGemvK) ? 256 * kMaxLoads * SK : kMaxGemvK;
+    /* the largest K this configuration is launched for: SK * NL group pairs */
+    constexpr int kMaxK = (256 * NL * SK < kMaxGemvK) ? 256 * NL * SK : kMaxGemvK;
     constexpr int kXIters = (kMaxK / 8 + W * 64 - 1) / (W * 64);
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
@@ -169,10 +170,10 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
         make_rsrc(wt + (size_t)(tile_ok ? tile : 0) * tile_bytes, tile_ok ? (uint32_t)tile_bytes : 0);
     const __amdgpu_buffer_rsrc_t sr =
         make_rsrc(st + (size_t)(tile_ok ? tile : 0) * G * 8, tile_ok ? (uint32_t)G * 16 : 0);
-    uint4 buf[kMaxLoads];
-    uint16_t sbits[kMaxLoads];
+    uint4 buf[NL];
+    uint16_t sbits[NL];
 #pragma unroll
-    for (int i = 0; i < kMaxLoads; ++i) {
+    for (int i = 0; i < NL; ++i) {
         const int p = ks + i * SK;
         const int g = 2 * p + half;
         const bool ok = p < P && g < G;
@@ -258,7 +259,7 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
      * the activation of the last group, so it adds exactly 0 without a branch */
     float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kMaxLoads; ++i) {
+    for (int i = 0; i < NL; ++i) {
         if (ks + i * SK < P) { /* wave-uniform */
             const int g = min(2 * (ks + i * SK) + half, G - 1);
             const uint4 *xq = smem4 + g * 16 + kb;
@@ -834,16 +835,16 @@ struct NormArgs {
     const uint16_t *sub = nullptr; /* plan F2: normalise BF16(x + sub) */
 };
 
-template <bool PAIR, bool OUT_F32, int TB, int SK>
+template <bool PAIR, bool OUT_F32, int TB, int SK, int NL>
 int launch_gemv_cfg(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N,
                     int K, hipStream_t stream, const NormArgs *norm = nullptr) {
     const int tiles = N / 8;
     if (norm)
-        hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK, true>),
+        hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK, true, NL>),
                            dim3((tiles + TB - 1) / TB), dim3(TB * SK * 64), gemv_smem(K, TB * SK),
                            stream, x, w, s, out, N, K, norm->w, norm->bias, norm->eps, norm->sub);
     else
-        hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK, false>),
+        hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK, false, NL>),
                            dim3((tiles + TB - 1) / TB), dim3(TB * SK * 64), gemv_smem(K, TB * SK),
                            stream, x, w, s, out, N, K, nullptr, 0.0f, 0.0f, nullptr);
     return hip_status(hipGetLastError(), "gemv launch");
@@ -894,9 +895,11 @@ int launch_xwave(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *o
  * - a long K (more group pairs than one wave holds, the down projection) runs the wave-local
  *   activation kernel: at K = 9728 / 8704 / 17408 it takes 5.85 / 8.35 / 12.9 us against
  *   6.2 / 9.7 / 15.7 us for the block-staged kernel;
- * - otherwise the block-staged kernel, split-K being the smallest power of two that keeps a
- *   wave at <= kMaxLoads pieces; a single-wave tile is split in two when it has more than six
- *   pairs (K = 2560 pair operand: 8.28 against 8.56 us). */
+ * - otherwise the block-staged kernel with few loads a wave (NL) and several waves a tile, which
+ *   keeps 8 waves a SIMD resident. Medians of 7 interleaved graph runs, whole C1 FFN (gate/up
+ *   shape varied, same down kernel): 2 tiles x 2 waves x 5 pairs 13.9 us; 1 x 4 x 3 14.4;
+ *   2 x 4 x 3 14.1; 4 x 1 x 10 14.7; 2 x 2 x 12 (12 loads a wave, 4 waves a SIMD) 14.9. At
+ *   K = 5120, 1 x 4 x 5 takes 19.8 us for the C4 FFN against 20.4 for 2 x 2 x 12. */
 template <bool PAIR, bool OUT_F32>
 int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N, int K,
                 hipStream_t stream, const NormArgs *norm = nullptr) {
@@ -905,19 +908,20 @@ int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *ou
         const int st = launch_xwave<OUT_F32>(x, w, s, out, N, K, stream);
         if (st <= 0) return st;
     }
-    int sk = 1;
-    while (sk < 16 && (pairs + sk - 1) / sk > kMaxLoads) sk *= 2;
-    switch (sk) {
-        case 1:
-            /* with the RMSNorm prologue every block normalises all of x: fewer, larger blocks */
-            if (pairs > 6 && !norm)
-                return launch_gemv_cfg<PAIR, OUT_F32, 2, 2>(x, w, s, out, N, K, stream, norm);
-            return launch_gemv_cfg<PAIR, OUT_F32, 4, 1>(x, w, s, out, N, K, stream, norm);
-        case 2: return launch_gemv_cfg<PAIR, OUT_F32, 2, 2>(x, w, s, out, N, K, stream, norm);
-        case 4: return launch_gemv_cfg<PAIR, OUT_F32, 2, 4>(x, w, s, out, N, K, stream, norm);
-        case 8: return launch_gemv_cfg<PAIR, OUT_F32, 1, 8>(x, w, s, out, N, K, stream, norm);
-        default: return launch_gemv_cfg<PAIR, OUT_F32, 1, 16>(x, w, s, out, N, K, stream, norm);
+    if (norm) {
+        /* every block normalises all of x: few, large blocks (one wave a tile, all of K) */
+        if (pairs <= 10) return launch_gemv_cfg<PAIR, OUT_F32, 4, 1, 10>(x, w, s, out, N, K, stream, norm);
+        if (pairs <= 12) return launch_gemv_cfg<PAIR, OUT_F32, 4, 1, 12>(x, w, s, out, N, K, stream, norm);
+        return set_error(W4A16_ERR_CONFIG, "gemv: the RMSNorm prologue needs K <= 3072");
     }
+    if (pairs <= 3) return launch_gemv_cfg<PAIR, OUT_F32, 4, 1, 3>(x, w, s, out, N, K, stream);
+    if (pairs <= 6) return launch_gemv_cfg<PAIR, OUT_F32, 2, 2, 3>(x, w, s, out, N, K, stream);
+    if (pairs <= 10) return launch_gemv_cfg<PAIR, OUT_F32, 2, 2, 5>(x, w, s, out, N, K, stream);
+    if (pairs <= 12) return launch_gemv_cfg<PAIR, OUT_F32, 2, 2, 6>(x, w, s, out, N, K, stream);
+    if (pairs <= 20) return launch_gemv_cfg<PAIR, OUT_F32, 1, 4, 5>(x, w, s, out, N, K, stream);
+    if (pairs <= 48) return launch_gemv_cfg<PAIR, OUT_F32, 1, 8, 6>(x, w, s, out, N, K, stream);
+    if (pairs <= 96) return launch_gemv_cfg<PAIR, OUT_F32, 1, 16, 6>(x, w, s, out, N, K, stream);
+    return launch_gemv_cfg<PAIR, OUT_F32, 1, 16, 8>(x, w, s, out, N, K, stream);
 }
 
 /* Split-K scratch for the MFMA form: FP32 partials and per-tile-pair arrival counters, one set
