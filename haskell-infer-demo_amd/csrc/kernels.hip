@@ -445,7 +445,10 @@ constexpr int kXwaveWaves = 16;
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kGMax = 20;       /* groups per wave (16-byte loads in flight per lane) */
+/* groups per wave (16-byte loads in flight per lane). 8 keeps the kernel near 80 VGPRs, so six
+ * waves a SIMD stay resident; medians of interleaved graph runs of the C1 FFN at M = 2/4/8/16:
+ * 20.0/22.2/23.9/30.1 us at 8 against 21.3/27.4/30.3/38.6 at 20 (4: 23.0/25.4/28.2/33.9). */
+constexpr int kGMax = 8;
 constexpr int kMfmaWaves = 4;   /* tile pairs per block */
 enum { kOutBf16 = 0, kOutPairSilu = 1, kOutF32 = 2 };
 
@@ -979,13 +982,11 @@ struct MfmaPlan {
 
 /* K split: at most kGMax groups per wave, activation range within 32 KiB of LDS, and enough
  * blocks that the waves cover the chip several times over. */
-int g_mfma_gmax = kGMax; /* groups per wave cap (tuning knob, <= kGMax) */
-
 MfmaPlan plan_mfma(int M, int N, int K) {
     MfmaPlan p{};
     const int G = K / 128;
     const int NT = (N / 8 + 1) / 2;
-    const int gmax = std::max(1, std::min(g_mfma_gmax, 128 / M));
+    const int gmax = std::max(1, std::min(kGMax, 128 / M));
     int S = (G + gmax - 1) / gmax;
     const int nblk = (NT + kMfmaWaves - 1) / kMfmaWaves;
     while ((long long)nblk * kMfmaWaves * S < 1024 && (G + S) / (S + 1) >= 4) ++S;
