@@ -912,9 +912,11 @@ int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *ou
         if (st <= 0) return st;
     }
     if (norm) {
-        /* every block normalises all of x: few, large blocks (one wave a tile, all of K) */
-        if (pairs <= 10) return launch_gemv_cfg<PAIR, OUT_F32, 4, 1, 10>(x, w, s, out, N, K, stream, norm);
-        if (pairs <= 12) return launch_gemv_cfg<PAIR, OUT_F32, 4, 1, 12>(x, w, s, out, N, K, stream, norm);
+        /* every block normalises all of x, yet the small-load shape still wins over fewer,
+         * larger blocks (C1 norm + FFN medians: 2 x 2 x 5 14.9 us, 4 x 1 x 10 15.4, 4 x 2 x 5
+         * 15.5; the FFN alone 13.9) */
+        if (pairs <= 10) return launch_gemv_cfg<PAIR, OUT_F32, 2, 2, 5>(x, w, s, out, N, K, stream, norm);
+        if (pairs <= 12) return launch_gemv_cfg<PAIR, OUT_F32, 2, 2, 6>(x, w, s, out, N, K, stream, norm);
         return set_error(W4A16_ERR_CONFIG, "gemv: the RMSNorm prologue needs K <= 3072");
     }
     if (pairs <= 3) return launch_gemv_cfg<PAIR, OUT_F32, 4, 1, 3>(x, w, s, out, N, K, stream);
