@@ -5,12 +5,21 @@
  * GEMVs: each lane loads one 16-byte piece (32 codes of one row) per step with a single
  * buffer_load_dwordx4, turns each pair of codes into a BF16 pair with a shift and one
  * v_bitop3_b32 (value 0.5 + u/32, u = nibble ^ 8 = code + 8, exact in BF16), and accumulates with
- * the packed BF16 dot product v_dot2_f32_bf16 against the activation pair. Since code = 32 v - 24, a piece's
- * contribution is 32 * dot(v, x) - 24 * sum(x); the per-piece activation sums are computed once
- * per block when the activation is staged in LDS. The
- * group's BF16 scale multiplies each piece's FP32 partial (the association of the reference's
- * tiled kernel, csrc/kernels/gemm_quant.cu:130-142). Lanes of one row are reduced with
- * cross-lane shuffles; the waves of a block (split-K over groups) through LDS.
+ * the packed BF16 dot product v_dot2_f32_bf16 against the activation pair. Since code = 32 v - 24,
+ * a piece's contribution is 32 * dot(v, x) - 24 * sum(x), with the per-piece activation sums
+ * formed once when the activation is staged in LDS. The group's BF16 scale multiplies each
+ * piece's FP32 partial (the association of the reference's tiled kernel,
+ * csrc/kernels/gemm_quant.cu:130-142). Lanes of one row are reduced with cross-lane shuffles.
+ *
+ *   gemv_tiles_kernel   M = 1, block-staged activation (gate/up with the fused SiLU x up
+ *                       epilogue, short-K linears); optional RMSNorm (and residual) prologue
+ *   gemv_xwave_kernel   M = 1, long K (the down projection): wave-local activation slices;
+ *                       optional residual epilogue
+ *   mfma_gemm_kernel    2 <= M <= 16: v_mfma_f32_16x16x32_bf16, K split across blocks
+ *   rmsnorm_kernel, residual_add_kernel, silu_mul_packed_kernel: the norm, the residual update
+ *                       and the standalone SiLU x up
+ *   tile_pack_kernel, dequant_tiled_kernel, quantize_kernel: the load-time re-layout and the
+ *                       checks of it
  */
 #include <hip/hip_runtime.h>
 
