@@ -139,3 +139,41 @@ def test_load_and_forward_tp2(cuda, model):
     total = oracle.bf16_bits((partials[0].astype(np.float64) + partials[1]).astype(np.float32))
     ref, _, _ = oracle.ffn_bf16(x, *arts[0], H, I)
     assert_parity(total, ref, "tp=2 partial sum vs full FFN", floor_div=16.0)
+
+
+def test_engine_rows_and_tp4(cuda, model):
+    """Verify rows through the engine (tokens = 4, 16: the MFMA form) at tp = 1, and rank 3 of
+    tp = 4 (slices of 2432 intermediate columns = 19 groups, reference csrc/engine.cu:2308-2395)
+    against the oracle on the same slice."""
+    import torch
+
+    out, arts = model
+    gup, gus, dp, ds = arts[1]
+    eng = w4a16.Engine(LAYERS, H, I, max_tokens=16)
+    assert eng.load_quantized_ffn(out) == 0, eng.last_error()
+    for tokens in (4, 16):
+        print(f"engine tokens={tokens}", flush=True)
+        x = oracle.synth_activation(tokens, H, 50 + tokens)
+        got = eng.forward(1, torch.from_numpy(x.view(np.int16)).to(cuda)).cpu().numpy()
+        ref, _, _ = oracle.ffn_bf16(x, gup, gus, dp, ds, H, I)
+        assert_parity(got.view(np.uint16), ref, f"engine rows={tokens}", floor_div=16.0)
+    eng.close()
+    tp, rank = 4, 3
+    li = I // tp
+    print("engine tp=4 rank 3", flush=True)
+    eng = w4a16.Engine(LAYERS, H, I, tp_size=tp, tp_rank=rank)
+    assert eng.load_quantized_ffn(out) == 0, eng.last_error()
+    rows = np.r_[rank * li:(rank + 1) * li, I + rank * li:I + (rank + 1) * li]
+    sgp, sgs = gup[rows], gus[rows]
+    sdp = np.ascontiguousarray(dp[:, rank * li // 2:(rank + 1) * li // 2])
+    sds = np.ascontiguousarray(ds[:, rank * li // 128:(rank + 1) * li // 128])
+    op = eng.operands(1)
+    deq = dequant_operand(op.down_packed, op.down_scales, H, li, False, cuda)
+    assert np.array_equal(deq.view(np.uint32),
+                          oracle.dequantize_numpy(sdp, sds, H, li).view(np.uint32))
+    x = oracle.synth_activation(1, H, 7)
+    part = eng.forward(1, torch.from_numpy(x.view(np.int16)).to(cuda), partial_f32=True)
+    want = oracle.ffn_partial_f32(x, sgp, sgs, sdp, sds, H, li)
+    rel = np.linalg.norm(part.cpu().numpy().astype(np.float64) - want) / np.linalg.norm(want)
+    assert rel <= 1e-3, rel
+    eng.close()
