@@ -37,7 +37,9 @@ namespace {
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kMaxLoads = 12;     /* group pairs one wave holds when it takes a whole tile (norm prologue) */
-constexpr int kMaxGemvK = 30464;  /* activation staged in LDS: 2K bytes + sums within 64 KiB */
+constexpr int kMaxGemvK = 30464;  /* block-staged GEMV: 2K bytes of activation + sums in 64 KiB */
+constexpr int kMaxRowK = 49152;   /* M = 1: the reference's limit (K * 2 <= 96 KiB of staging) */
+constexpr int kMaxAnyK = 1 << 20; /* M > 1 (the MFMA form stages only its K range) */
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
@@ -899,6 +901,9 @@ int launch_xwave(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *o
         case 3: return launch_xwave_np<OUT_F32, 3, 8, 3>(x, w, s, out, N, K, stream, residual, sub);
         case 4: return launch_xwave_np<OUT_F32, 3, 8, 4>(x, w, s, out, N, K, stream, residual, sub);
         case 5: return launch_xwave_np<OUT_F32, 3, 8, 5>(x, w, s, out, N, K, stream, residual, sub);
+        case 6: return launch_xwave_np<OUT_F32, 3, 8, 6>(x, w, s, out, N, K, stream, residual, sub);
+        case 7: return launch_xwave_np<OUT_F32, 3, 8, 7>(x, w, s, out, N, K, stream, residual, sub);
+        case 8: return launch_xwave_np<OUT_F32, 3, 8, 8>(x, w, s, out, N, K, stream, residual, sub);
         default: return 1;
     }
 }
@@ -1068,9 +1073,15 @@ int check_gemm_args(const void *a, const void *p, const void *s, const void *o, 
     if (N % W4A16_TILE_ROWS != 0)
         return set_error(W4A16_ERR_CONFIG, "%s: N=%d is not a whole number of 8-row tiles",
                          what, N);
-    if (K > kMaxGemvK)
-        return set_error(W4A16_ERR_CONFIG, "%s: K=%d needs more activation staging than one "
-                         "block has (max %d)", what, K, kMaxGemvK);
+    if (M == 1 && K > kMaxRowK)
+        return set_error(W4A16_ERR_CONFIG, "%s: K=%d at M=1 needs more than 96 KiB of activation "
+                         "staging (max K %d)", what, K, kMaxRowK);
+    if (K > kMaxAnyK)
+        return set_error(W4A16_ERR_CONFIG, "%s: K=%d exceeds this build's limit %d", what, K,
+                         kMaxAnyK);
+    if ((unsigned long long)N * (unsigned long long)K / 2 >= (1ull << 32))
+        return set_error(W4A16_ERR_CONFIG, "%s: a %d x %d operand exceeds the 4 GiB a buffer "
+                         "descriptor addresses", what, N, K);
     return 0;
 }
 
@@ -1093,8 +1104,11 @@ static int run_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *
         const int rows = std::min(16, M - m0);
         const uint16_t *xs = x + (size_t)m0 * K;
         void *os = static_cast<char *>(out) + (size_t)m0 * out_cols * out_elem;
-        const int st = rows == 1 ? launch_gemv<PAIR, F32>(xs, w, s, os, N, K, stream)
-                                 : launch_mfma<OUT>(xs, rows, w, s, os, N, K, stream);
+        /* one row: the v_dot2 GEMVs, except a pair operand past the block-staged kernel's K
+         * (then the MFMA form with one live row) */
+        const bool gemv = rows == 1 && (!PAIR || K <= kMaxGemvK);
+        const int st = gemv ? launch_gemv<PAIR, F32>(xs, w, s, os, N, K, stream)
+                            : launch_mfma<OUT>(xs, rows, w, s, os, N, K, stream);
         if (st) return st;
     }
     return W4A16_OK;

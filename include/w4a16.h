@@ -102,7 +102,9 @@ int w4a16_quantize_device(long long n, long long k, const float *weights, uint8_
 
 /* out[M, N] (BF16) = a[M, K] (BF16) x W^T, FP32 accumulation, W in tile order (pair = 0).
  * Same refusals as the reference wrapper: M,N < 0, K <= 0 or group <= 0; M == 0 or N == 0 is a
- * no-op; null buffers; K % group; group % 8. Replaces gemm_int4_bf16 (reference
+ * no-op; null buffers; K % group; group % 8; at M = 1, K * 2 > 96 KiB (K > 49152). The tile
+ * order adds N % 8 and group == 128 (both always true of the format's artifacts), and this build
+ * refuses K > 2^20 and an operand of 4 GiB or more. Replaces gemm_int4_bf16 (reference
  * csrc/include/layers.h:376-377, csrc/kernels/gemm_quant.cu:204-254), which throws instead. */
 int gemm_int4_bf16(const uint16_t *a, const uint8_t *packed, const uint16_t *scales,
                    uint16_t *out, int M, int N, int K, int group, void *stream);

@@ -161,3 +161,17 @@ def test_residual_norm_entry_refusals_without_touching_the_device():
         w4a16.W4A16_ERR_CONFIG
     assert lib.mlp_int4_residual_norm_bf16(d, d, d, 1, 1e-6, *w, d, d, 0, 2560, 9728, None) == \
         w4a16.W4A16_OK
+
+
+def test_gemm_shape_limits_without_touching_the_device():
+    """The reference wrapper refuses M = 1 with K * 2 > 96 KiB (csrc/kernels/gemm_quant.cu:228-231);
+    so does gemm_int4_bf16, before any device call. This build also refuses K > 2^20 and an operand
+    of 4 GiB or more (32-bit buffer descriptors)."""
+    lib = w4a16.lib
+    d = 16
+    assert lib.gemm_int4_bf16(d, d, d, d, 1, 64, 49280, 128, None) == w4a16.W4A16_ERR_CONFIG
+    assert "96 KiB" in w4a16.last_error()
+    assert lib.gemm_int4_bf16(d, d, d, d, 2, 64, (1 << 20) + 128, 128, None) == \
+        w4a16.W4A16_ERR_CONFIG
+    assert lib.gemm_int4_bf16(d, d, d, d, 2, 65536, 131072, 128, None) == w4a16.W4A16_ERR_CONFIG
+    assert "4 GiB" in w4a16.last_error()

@@ -101,7 +101,9 @@ def test_quantize_device_bit_exact(cuda):
                                  (256, 128), (1024, 384), (24, 1152),
                                  # wave-local kernel with an odd group count (13 pairs, NP = 1),
                                  # its widest slice (NP = 7), and past it (block-staged, SK = 16)
-                                 (64, 3200), (40, 28672), (16, 30464)])
+                                 (64, 3200), (40, 28672), (16, 30464),
+                                 # the reference's M = 1 limit (K * 2 = 96 KiB): 8 blocks a tile
+                                 (64, 49152)])
 def test_gemv_parity(cuda, n, k):
     say(f"gemv n={n} k={k}")
     p, s = make_weight(n, k, seed=n + k)
@@ -123,6 +125,26 @@ def test_small_m_parity(cuda, m):
     w = w4a16.TiledWeight.from_artifact(p, s, n, k, device=cuda)
     out = from_dev(w4a16.gemm_int4_bf16(to_dev(x, cuda), w))
     assert_parity(out, oracle.gemm_bf16(x, p, s, n, k), f"gemm M={m}")
+
+
+def test_long_k_routes(cuda):
+    """K past the block-staged kernel: a pair operand at M = 1 (hidden 32768) runs the MFMA form
+    with one live row; M = 4 at K = 65536 (the MFMA form, 64 K splits)."""
+    k, inter = 32768, 64
+    say(f"gate/up pair M=1 K={k}")
+    gp, gs = make_weight(2 * inter, k, seed=5)
+    x = oracle.synth_activation(1, k, seed=8)
+    gu = w4a16.TiledWeight.from_artifact(gp, gs, 2 * inter, k, pair=True, device=cuda)
+    act = from_dev(w4a16.gate_up_silu(to_dev(x, cuda), gu))
+    mid = oracle.gemm_bf16(x, gp, gs, 2 * inter, k)
+    assert_parity(act, oracle.silu_mul_packed(mid, 1, inter), f"gate/up K={k}")
+    n, k, m = 64, 65536, 4
+    say(f"gemm M={m} K={k}")
+    p, s = make_weight(n, k, seed=6)
+    x = oracle.synth_activation(m, k, seed=9)
+    w = w4a16.TiledWeight.from_artifact(p, s, n, k, device=cuda)
+    out = from_dev(w4a16.gemm_int4_bf16(to_dev(x, cuda), w))
+    assert_parity(out, oracle.gemm_bf16(x, p, s, n, k), f"gemm M={m} K={k}")
 
 
 def test_gemv_closed_forms(cuda):
