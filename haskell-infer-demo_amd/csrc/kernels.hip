@@ -15,6 +15,8 @@
  *                       epilogue, short-K linears); optional RMSNorm (and residual) prologue
  *   gemv_xwave_kernel   M = 1, long K (the down projection): wave-local activation slices;
  *                       optional residual epilogue
+ *   gemv_rows_kernel    2 <= M <= 8: the GEMV's block structure on v_mfma_f32_16x16x32_bf16 with
+ *                       a block-diagonal operand, activation loaded straight into LDS
  *   mfma_gemm_kernel    2 <= M <= 16: v_mfma_f32_16x16x32_bf16, K split across blocks
  *   rmsnorm_kernel, residual_add_kernel, silu_mul_packed_kernel: the norm, the residual update
  *                       and the standalone SiLU x up
@@ -40,6 +42,7 @@ constexpr int kMaxLoads = 12;     /* group pairs one wave holds when it takes a 
 constexpr int kMaxGemvK = 30464;  /* block-staged GEMV: 2K bytes of activation + sums in 64 KiB */
 constexpr int kMaxRowK = 49152;   /* M = 1: the reference's limit (K * 2 <= 96 KiB of staging) */
 constexpr int kMaxAnyK = 1 << 20; /* M > 1 (the MFMA form stages only its K range) */
+constexpr size_t kMaxLds = 163840; /* LDS a block can allocate on gfx950 */
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
@@ -115,6 +118,13 @@ __device__ __forceinline__ uint16_t buf_load_u16(__amdgpu_buffer_rsrc_t r, uint3
 }
 
 constexpr uint32_t kOob = 0x80000000u; /* an offset no buffer here reaches: reads return 0 */
+
+/* s_waitcnt immediate that waits until at most N vector memory operations are outstanding
+ * (vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at their maxima, i.e. not waited on):
+ * with the NL weight and NL scale loads of a wave issued last, N = 2 NL waits for everything
+ * issued before them. */
+template <int NL>
+constexpr int kVmcntWeights = ((2 * NL) & 15) | (7 << 4) | (15 << 8) | (((2 * NL) >> 4) << 14);
 
 /* A block holds TB consecutive 8-row tiles and W = TB * SK waves: wave w works on tile w / SK and
  * takes the group pairs (w % SK) + SK * i of it; half-wave h of a step takes group 2 * pair + h.
@@ -654,6 +664,146 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
     }
 }
 
+/* ------------------------------------------------------------------------------------------
+ * Few rows (2 <= M <= 8) on the GEMV's block structure: TB tiles a block, SK waves a tile, NL
+ * group pairs a wave, the activation staged in LDS once per block, no split-K across blocks.
+ * The inner product runs on v_mfma_f32_16x16x32_bf16 with a block-diagonal operand: lane l
+ * loads the 16-byte piece (row r = l & 7, kb = q = l >> 4) of group 2p + a, a = (l >> 3) & 1, so
+ * B column n = 8a + r is tile row r of one group of the pair and the 32-wide k block of MFMA t
+ * (the piece's dword t) is k = 32 t + 8 kb + j in both groups. A row 8a + m holds activation row
+ * m of group 2p + a at the same k, so D[8a + m][8a + r] is row r's group sum for row m (the other
+ * quadrants mix the groups and are not used). B holds 0.75 + code/32; four more MFMAs against a
+ * constant -0.75 operand take the offset out inside the accumulator, so the VALU only unpacks
+ * codes and applies the scale. Lane l's D rows are 4q + i (a = q >> 1, m = 4 (q & 1) + i);
+ * lanes l and l ^ 40 hold the two groups of a pair for the same (r, m).
+ *
+ * The activation goes from memory straight into LDS (buffer_load ... lds, 16 bytes a lane),
+ * every load issued before the weight loads, in the order [pair][16-byte chunk c][row m][a]:
+ * the 16 lanes of one ds_read_b128 pass (one k block, rows 8a + m) then read 16 consecutive
+ * chunks, which covers every bank once. Chunks of a group past K are loaded as zeros.
+ * ---------------------------------------------------------------------------------------- */
+template <bool PAIR, bool OUT_F32, int TB, int SK, int NL, int MI>
+__global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
+    const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K) {
+    constexpr int W = TB * SK;
+    extern __shared__ uint4 smem4[];
+    const int G = K >> 7;
+    const int P = (G + 1) >> 1;
+    const int tiles = N >> 3;
+    const int cpr = K >> 3;             /* 16-byte chunks a row in memory */
+    const int nlds = P * 32 * M;        /* staged chunks (both groups of every pair) */
+    const int nins = (nlds + 63) >> 6;  /* 1 KiB load instructions */
+    float *red = reinterpret_cast<float *>(smem4 + nins * 64); /* [W][8 rows][8 tile rows] */
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = blockIdx.x * TB + wave / SK;
+    const int ks = wave % SK;
+    const int q = lane >> 4;
+    const int a = (lane >> 3) & 1;
+    const int r = lane & 7;
+
+    /* 1. the activation, straight into LDS: instruction j of the block (wave j % W) fills
+     * staged chunks 64 j .. 64 j + 63 */
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)M * cpr * 16);
+    int xloads = 0;
+    for (int j = wave; j < nins; j += W) {
+        const int pos = j * 64 + lane;
+        const int t2 = pos >> 1;
+        const int m = t2 % M;
+        const int t3 = t2 / M;
+        const int g = 2 * (t3 >> 4) + (pos & 1);
+        const bool ok = pos < nlds && g < G;
+        const uint32_t off = ok ? (uint32_t)((m * cpr + g * 16 + (t3 & 15)) * 16) : kOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xr, (__attribute__((address_space(3))) void *)(smem4 + j * 64), 16, off, 0, 0, 0);
+        ++xloads;
+    }
+
+    /* 2. every weight piece and scale of this wave */
+    const bool tile_ok = tile < tiles;
+    const size_t tile_bytes = (size_t)G * 512;
+    const __amdgpu_buffer_rsrc_t wr =
+        make_rsrc(wt + (size_t)(tile_ok ? tile : 0) * tile_bytes, tile_ok ? (uint32_t)tile_bytes : 0);
+    const __amdgpu_buffer_rsrc_t sr =
+        make_rsrc(st + (size_t)(tile_ok ? tile : 0) * G * 8, tile_ok ? (uint32_t)G * 16 : 0);
+    uint4 buf[NL];
+    uint16_t sbits[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int p = ks + i * SK;
+        const int g = 2 * p + a;
+        const bool ok = p < P && g < G;
+        buf[i] = buf_load16(wr, ok ? (uint32_t)(g * 512 + (q * 8 + r) * 16) : kOob);
+        sbits[i] = buf_load_u16(sr, ok ? (uint32_t)(g * 16 + r * 2) : kOob);
+    }
+
+    /* 3. wait for this wave's activation loads only (issued first; memory ops complete in
+     * order of the counter), then for every wave's */
+    (void)xloads;
+    __builtin_amdgcn_s_waitcnt(kVmcntWeights<NL>);
+    __syncthreads();
+
+    /* 4. eight MFMAs a pair. A piece past the tile's groups has scale 0 (its loads read 0) and
+     * its staged activation is zero, so it adds exactly 0 without a branch; lanes of A rows
+     * m >= M read row M - 1 (their D rows are not used). */
+    const uint4 *abase = smem4 + (q * M + min(r, M - 1)) * 2 + a;
+    const uint4 offs = make_uint4(0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u);
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int p = ks + i * SK;
+        if (p < P) { /* wave-uniform */
+            const uint4 *xa = abase + p * 32 * M;
+            const uint32_t words[4] = {buf[i].x, buf[i].y, buf[i].z, buf[i].w};
+            f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xa[t * 8 * M]);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, unpack8(words[t]), d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, offs),
+                                                            d, 0, 0, 0);
+            }
+            const float sc = bf16_widen(sbits[i]);
+#pragma unroll
+            for (int j = 0; j < MI; ++j) acc[j] = fmaf(sc, d[j], acc[j]);
+        }
+    }
+
+    /* 5. the pair's two groups (lanes l, l ^ 40), then the SK waves of a tile in LDS; the
+     * code step 1/32 is applied once here (a power of two: exact) */
+#pragma unroll
+    for (int j = 0; j < MI; ++j) acc[j] = 32.0f * (acc[j] + __shfl_xor(acc[j], 40));
+    if ((lane & 40) == 0) {
+#pragma unroll
+        for (int j = 0; j < MI; ++j) red[wave * 64 + (4 * q + j) * 8 + r] = acc[j];
+    }
+    __syncthreads();
+    if (ks != 0 || !tile_ok) return;
+    const int m = lane >> 3;
+    float row_sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < SK; ++w) row_sum += red[(wave + w) * 64 + lane];
+    if (PAIR) {
+        /* lane r < 4 of row m has gate row r, lane r + 4 the matching up row */
+        const float upv = __shfl_down(row_sum, 4);
+        if (r < 4 && m < M) {
+            const float gate = bf16_widen(bf16_rne(row_sum));
+            const float up = bf16_widen(bf16_rne(upv));
+            reinterpret_cast<uint16_t *>(out)[(size_t)m * (N >> 1) + tile * 4 + r] =
+                silu_mul_bf16(gate, up);
+        }
+    } else if (m < M) {
+        const size_t o = (size_t)m * N + tile * 8 + r;
+        if (OUT_F32)
+            reinterpret_cast<float *>(out)[o] = row_sum;
+        else
+            reinterpret_cast<uint16_t *>(out)[o] = bf16_rne(row_sum);
+    }
+}
+
 /* RMSNorm of each row (one block a row): BF16(x * rsqrt(sum x^2 / cols + eps) * (bias + w)),
  * FP32 arithmetic (reference csrc/kernels/flashinfer_norm.cu:22-76). Each thread holds CH
  * 8-value chunks of the row, all loaded before any use, so a row costs one load round trip;
@@ -943,6 +1093,59 @@ int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *ou
     return launch_gemv_cfg<PAIR, OUT_F32, 1, 16, 8>(x, w, s, out, N, K, stream);
 }
 
+/* Few-row kernel: LDS for both groups of every pair of the M rows (whole 1 KiB load
+ * instructions) and the wave reduction. */
+size_t rows_smem(int M, int K, int waves) {
+    const int P = (K / 128 + 1) / 2;
+    return (size_t)((P * 32 * M + 63) / 64) * 1024 + (size_t)waves * 256;
+}
+
+template <bool PAIR, bool OUT_F32, int TB, int SK, int NL>
+int launch_rows_mi(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
+                   int N, int K, hipStream_t stream) {
+    const size_t smem = rows_smem(M, K, TB * SK);
+    if (smem > kMaxLds) return 1;
+    const dim3 grid((N / 8 + TB - 1) / TB), block(TB * SK * 64);
+    if (M == 2)
+        hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 2>), grid, block, smem,
+                           stream, x, M, w, s, out, N, K);
+    else
+        hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 4>), grid, block, smem,
+                           stream, x, M, w, s, out, N, K);
+    return hip_status(hipGetLastError(), "gemv rows launch");
+}
+
+/* 2 <= M <= 8 on the few-row kernel; returns 1 when the shape is not applicable (the staged
+ * rows past the LDS of a block, or more than 80 group pairs). Shapes from sweeps of the C1 FFN
+ * (graph-replayed, weights rotated past the MALL; gate/up K = 2560, down K = 9728):
+ * - short K (gate/up): the M = 1 GEMV's shapes up to M = 4; from M = 5 twice the tiles a block,
+ *   which halves the activation staged per tile (M = 8: 4 x 2 x 5 11.0 us, 2 x 2 x 5 12.0);
+ * - long K (down): two tiles of eight waves a block (M = 2 / 4 / 8: 6.6 / 7.8 / 9.3 us; one tile
+ *   of 8 or 16 waves: 7.0 / 8.8-9.1 / 14.3, the M = 8 rows filling 155 KB of LDS a block). */
+template <bool PAIR, bool OUT_F32>
+int launch_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
+                int K, hipStream_t stream) {
+    if (M < 2 || M > 8) return 1;
+    const int pairs = (K / 128 + 1) / 2;
+    if (pairs <= 12 && M <= 4) {
+        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 4, 1, 3>(x, M, w, s, out, N, K, stream);
+        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 3>(x, M, w, s, out, N, K, stream);
+        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 5>(x, M, w, s, out, N, K, stream);
+        return launch_rows_mi<PAIR, OUT_F32, 2, 2, 6>(x, M, w, s, out, N, K, stream);
+    }
+    if (pairs <= 12) {
+        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 8, 1, 3>(x, M, w, s, out, N, K, stream);
+        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 3>(x, M, w, s, out, N, K, stream);
+        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 5>(x, M, w, s, out, N, K, stream);
+        return launch_rows_mi<PAIR, OUT_F32, 4, 2, 6>(x, M, w, s, out, N, K, stream);
+    }
+    if (pairs <= 20) return launch_rows_mi<PAIR, OUT_F32, 2, 4, 5>(x, M, w, s, out, N, K, stream);
+    if (pairs <= 40) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 5>(x, M, w, s, out, N, K, stream);
+    if (pairs <= 48) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 6>(x, M, w, s, out, N, K, stream);
+    if (pairs <= 80) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 10>(x, M, w, s, out, N, K, stream);
+    return 1;
+}
+
 /* Split-K scratch for the MFMA form: FP32 partials and per-tile-pair arrival counters, one set
  * per device, grown on demand (growth synchronises the device; counters are zeroed when
  * allocated and every kernel leaves them zero). Calls that overlap in time on one device share
@@ -1091,8 +1294,9 @@ int check_gemm_args(const void *a, const void *p, const void *s, const void *o, 
 /* C ABI                                                                                     */
 /* ---------------------------------------------------------------------------------------- */
 
-/* Rows of x: M = 1 takes the v_dot2 GEMV; 2 <= M <= 16 the MFMA form (one pass over the weight
- * for all rows); larger M runs the MFMA form on 16-row slices. */
+/* Rows of x: M = 1 takes the v_dot2 GEMV; 2 <= M <= 8 the few-row MFMA kernel where its staged
+ * rows fit a block's LDS, otherwise (and for 9 <= M <= 16) the split-K MFMA form, one pass over
+ * the weight for all rows; larger M runs on 16-row slices. */
 template <int OUT>
 static int run_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
                     int N, int K, hipStream_t stream) {
@@ -1107,8 +1311,9 @@ static int run_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *
         /* one row: the v_dot2 GEMVs, except a pair operand past the block-staged kernel's K
          * (then the MFMA form with one live row) */
         const bool gemv = rows == 1 && (!PAIR || K <= kMaxGemvK);
-        const int st = gemv ? launch_gemv<PAIR, F32>(xs, w, s, os, N, K, stream)
-                            : launch_mfma<OUT>(xs, rows, w, s, os, N, K, stream);
+        int st = gemv ? launch_gemv<PAIR, F32>(xs, w, s, os, N, K, stream)
+                      : launch_rows<PAIR, F32>(xs, rows, w, s, os, N, K, stream);
+        if (st > 0) st = launch_mfma<OUT>(xs, rows, w, s, os, N, K, stream);
         if (st) return st;
     }
     return W4A16_OK;

@@ -127,6 +127,29 @@ def test_small_m_parity(cuda, m):
     assert_parity(out, oracle.gemm_bf16(x, p, s, n, k), f"gemm M={m}")
 
 
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 6, 7, 8])
+def test_few_rows_parity(cuda, m):
+    """2 <= M <= 8 on the few-row MFMA kernel, through each of its block shapes: 1 group pair,
+    an odd group count with a half-filled block of tiles, 10, 13 (odd) and 38 pairs; the last
+    falls back to the split-K MFMA form once the staged rows pass 64 KiB of LDS (M >= 4). The
+    gate/up pair with the fused SiLU epilogue at an odd group count."""
+    for n, k in [(256, 256), (24, 1152), (2560, 2560), (64, 3200), (640, 9728)]:
+        say(f"gemm M={m} n={n} k={k}")
+        p, s = make_weight(n, k, seed=n + k + m)
+        x = oracle.synth_activation(m, k, seed=200 + m)
+        w = w4a16.TiledWeight.from_artifact(p, s, n, k, device=cuda)
+        out = from_dev(w4a16.gemm_int4_bf16(to_dev(x, cuda), w))
+        assert_parity(out, oracle.gemm_bf16(x, p, s, n, k), f"gemm M={m} {n}x{k}")
+    hidden, inter = 1152, 72
+    say(f"gate/up M={m} H={hidden} I={inter}")
+    gp, gs = make_weight(2 * inter, hidden, seed=300 + m)
+    x = oracle.synth_activation(m, hidden, seed=400 + m)
+    gu = w4a16.TiledWeight.from_artifact(gp, gs, 2 * inter, hidden, pair=True, device=cuda)
+    act = from_dev(w4a16.gate_up_silu(to_dev(x, cuda), gu))
+    mid = oracle.gemm_bf16(x, gp, gs, 2 * inter, hidden)
+    assert_parity(act, oracle.silu_mul_packed(mid, m, inter), f"gate/up M={m}")
+
+
 def test_long_k_routes(cuda):
     """K past the block-staged kernel: a pair operand at M = 1 (hidden 32768) runs the MFMA form
     with one live row; M = 4 at K = 65536 (the MFMA form, 64 K splits)."""
