@@ -262,7 +262,8 @@ def main():
 
             f2_us, _, _ = timed(capture(f2_call), args.steps, args.warmup)
     args.steps = calls
-    family = "gemv_tiles_kernel" if m == 1 else "mfma_gemm_kernel"
+    family = ("gemv_tiles_kernel" if m == 1 else "gemv_rows_kernel" if m <= 8
+              else "mfma_gemm_kernel")
     if linear_only:
         dom_bytes = per_set
         dom_name = f"{family} (gemm_int4_bf16)"
@@ -278,9 +279,10 @@ def main():
         # (FETCH_SIZE and WRITE_SIZE scaled by a plain copy of known size).
         with open(tpath) as handle:
             entries = json.load(handle).get(tag, {})
-        prefix = ("gemv_tiles_kernel<false, false" if linear_only else "gemv_tiles_kernel<true, false")
-        if m != 1:
+        if family == "mfma_gemm_kernel":
             prefix = "mfma_gemm_kernel<0" if linear_only else "mfma_gemm_kernel<1"
+        else:
+            prefix = f"{family}<false, false" if linear_only else f"{family}<true, false"
         for kname, entry in entries.items():
             if kname.startswith(prefix):
                 traffic, traffic_src = entry["traffic_bytes"], os.path.relpath(tpath, ROOT)
