@@ -103,7 +103,9 @@ def test_quantize_device_bit_exact(cuda):
                                  # its widest slice (NP = 7), and past it (block-staged, SK = 16)
                                  (64, 3200), (40, 28672), (16, 30464),
                                  # the reference's M = 1 limit (K * 2 = 96 KiB): 8 blocks a tile
-                                 (64, 49152)])
+                                 (64, 49152),
+                                 # wave-local kernel, one pair a wave, 288 and 384 tiles
+                                 (2304, 4096), (3072, 4096)])
 def test_gemv_parity(cuda, n, k):
     say(f"gemv n={n} k={k}")
     p, s = make_weight(n, k, seed=n + k)
