@@ -263,7 +263,7 @@ def main():
             f2_us, _, _ = timed(capture(f2_call), args.steps, args.warmup)
     args.steps = calls
     family = ("gemv_tiles_kernel" if m == 1 else "gemv_rows_kernel" if m <= 8
-              else "mfma_gemm_kernel")
+              else "gemv_rows16_kernel" if m <= 16 else "mfma_gemm_kernel")
     if linear_only:
         dom_bytes = per_set
         dom_name = f"{family} (gemm_int4_bf16)"

@@ -17,7 +17,9 @@
  *                       optional residual epilogue
  *   gemv_rows_kernel    2 <= M <= 8: the GEMV's block structure on v_mfma_f32_16x16x32_bf16 with
  *                       a block-diagonal operand, activation loaded straight into LDS
- *   mfma_gemm_kernel    2 <= M <= 16: v_mfma_f32_16x16x32_bf16, K split across blocks
+ *   gemv_rows16_kernel  9 <= M <= 16, short K: the same with a tile pair a wave
+ *   mfma_gemm_kernel    2 <= M <= 16 where the above do not fit: v_mfma_f32_16x16x32_bf16, K
+ *                       split across blocks
  *   rmsnorm_kernel, residual_add_kernel, silu_mul_packed_kernel: the norm, the residual update
  *                       and the standalone SiLU x up
  *   tile_pack_kernel, dequant_tiled_kernel, quantize_kernel: the load-time re-layout and the
@@ -804,6 +806,122 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
     }
 }
 
+/* Up to 16 rows (9 <= M <= 16), short K: as gemv_rows_kernel, but a wave owns a tile pair and a
+ * load covers one group of both tiles (lane l: piece (row l & 7, kb = l >> 4) of tile
+ * 2 tp + ((l >> 3) & 1)), so all sixteen B columns share the k range and all sixteen A rows are
+ * activation rows. A block holds blockDim / 64 waves: TP tile pairs of SK waves (both runtime),
+ * NL groups a wave (group ks + i SK); the rows are staged in the order [group][chunk][row], so
+ * the 16 lanes of one ds_read_b128 pass read 16 consecutive chunks. */
+template <bool PAIR, bool OUT_F32, int NL>
+__global__ __launch_bounds__(1024) void gemv_rows16_kernel(
+    const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, int TP, int SK) {
+    const int W = TP * SK;
+    extern __shared__ uint4 smem4[];
+    const int G = K >> 7;
+    const int tiles = N >> 3;
+    const int cpr = K >> 3;
+    const int nlds = G * 16 * M;
+    const int nins = (nlds + 63) >> 6;
+    f32x4_t *red = reinterpret_cast<f32x4_t *>(smem4 + nins * 64); /* [W][64 lanes] */
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tp = blockIdx.x * TP + wave / SK;
+    const int ks = wave % SK;
+    const int q = lane >> 4;
+    const int n = lane & 15;
+    const int r = n & 7;
+    const int tile = 2 * tp + (n >> 3);
+
+    /* 1. the activation, straight into LDS */
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)M * cpr * 16);
+    for (int j = wave; j < nins; j += W) {
+        const int pos = j * 64 + lane;
+        const int m = pos % M;
+        const int t2 = pos / M;
+        const uint32_t off =
+            pos < nlds ? (uint32_t)((m * cpr + (t2 >> 4) * 16 + (t2 & 15)) * 16) : kOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xr, (__attribute__((address_space(3))) void *)(smem4 + j * 64), 16, off, 0, 0, 0);
+    }
+
+    /* 2. every weight piece and scale of this wave (a tile past N reads zeros) */
+    const bool tile_ok = tile < tiles;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wt, (uint32_t)((size_t)N * K / 2));
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(st, (uint32_t)((size_t)N * G * 2));
+    uint4 buf[NL];
+    uint16_t sbits[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int g = ks + i * SK;
+        const bool ok = tile_ok && g < G;
+        const uint32_t unit = (uint32_t)(tile * G + g);
+        buf[i] = buf_load16(wr, ok ? unit * 512 + (uint32_t)(q * 8 + r) * 16 : kOob);
+        sbits[i] = buf_load_u16(sr, ok ? unit * 16 + (uint32_t)r * 2 : kOob);
+    }
+    __builtin_amdgcn_s_waitcnt(kVmcntWeights<NL>);
+    __syncthreads();
+
+    /* 3. eight MFMAs a group (the offset ones as in gemv_rows_kernel) */
+    const uint4 *abase = smem4 + q * M + min(n, M - 1);
+    const uint4 offs = make_uint4(0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u);
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int g = ks + i * SK;
+        if (g < G) { /* wave-uniform */
+            const uint4 *xa = abase + g * 16 * M;
+            const uint32_t words[4] = {buf[i].x, buf[i].y, buf[i].z, buf[i].w};
+            f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xa[t * 4 * M]);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, unpack8(words[t]), d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, offs),
+                                                            d, 0, 0, 0);
+            }
+            const float sc = bf16_widen(sbits[i]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = fmaf(sc, d[j], acc[j]);
+        }
+    }
+
+    /* 4. the SK waves of a tile pair in LDS; lane (n, q) then holds rows 4 q + j of column n */
+    red[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (ks != 0) return;
+    f32x4_t sum = red[wave * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < SK; ++w) {
+        const f32x4_t v = red[(wave + w) * 64 + lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sum[j] += v[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float row_sum = 32.0f * sum[j];
+        const int m = 4 * q + j;
+        if (PAIR) {
+            /* column r < 4 of a tile has gate row r, column r + 4 the matching up row */
+            const float upv = __shfl_down(row_sum, 4);
+            if (r < 4 && m < M && tile_ok) {
+                const float gate = bf16_widen(bf16_rne(row_sum));
+                const float up = bf16_widen(bf16_rne(upv));
+                reinterpret_cast<uint16_t *>(out)[(size_t)m * (N >> 1) + tile * 4 + r] =
+                    silu_mul_bf16(gate, up);
+            }
+        } else if (m < M && tile_ok) {
+            const size_t o = (size_t)m * N + tile * 8 + r;
+            if (OUT_F32)
+                reinterpret_cast<float *>(out)[o] = row_sum;
+            else
+                reinterpret_cast<uint16_t *>(out)[o] = bf16_rne(row_sum);
+        }
+    }
+}
+
 /* RMSNorm of each row (one block a row): BF16(x * rsqrt(sum x^2 / cols + eps) * (bias + w)),
  * FP32 arithmetic (reference csrc/kernels/flashinfer_norm.cu:22-76). Each thread holds CH
  * 8-value chunks of the row, all loaded before any use, so a row costs one load round trip;
@@ -1122,9 +1240,48 @@ int launch_rows_mi(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s
  *   which halves the activation staged per tile (M = 8: 4 x 2 x 5 11.0 us, 2 x 2 x 5 12.0);
  * - long K (down): two tiles of eight waves a block (M = 2 / 4 / 8: 6.6 / 7.8 / 9.3 us; one tile
  *   of 8 or 16 waves: 7.0 / 8.8-9.1 / 14.3, the M = 8 rows filling 155 KB of LDS a block). */
+/* 9 <= M <= 16, short K: tile-pair waves. Each block stages all M rows (80 KB at M = 16,
+ * K = 2560, so at most two blocks a CU), which makes the grid's balance the lever: one block a
+ * CU, TP = ceil(tile pairs / CUs) tile pairs of SK = 16 / TP waves. C1 gate/up at M = 16
+ * (1216 tile pairs): 5 x 3 waves 11.7 us; 6 x 2 11.9, 5 x 2 12.1, 8 x 2 13.4, 3 x 5 14.8,
+ * 4 x 4 17.0, 2 x 8 17.6, 1 x 4 24.4 (the split-K MFMA form: 16.3). */
+size_t rows16_smem(int M, int K, int waves) {
+    return (size_t)((K / 128 * 16 * M + 63) / 64) * 1024 + (size_t)waves * 1024;
+}
+
+template <bool PAIR, bool OUT_F32, int NL>
+int launch_rows16_nl(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
+                     int N, int K, int TP, int SK, hipStream_t stream) {
+    const size_t smem = rows16_smem(M, K, TP * SK);
+    if (smem > kMaxLds) return 1;
+    const int pairs = (N / 8 + 1) / 2;
+    hipLaunchKernelGGL((gemv_rows16_kernel<PAIR, OUT_F32, NL>), dim3((pairs + TP - 1) / TP),
+                       dim3(TP * SK * 64), smem, stream, x, M, w, s, out, N, K, TP, SK);
+    return hip_status(hipGetLastError(), "gemv rows16 launch");
+}
+
+int device_cus();
+
+template <bool PAIR, bool OUT_F32>
+int launch_rows16(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
+                  int K, hipStream_t stream) {
+    const int G = K / 128;
+    const int pairs = (N / 8 + 1) / 2;
+    const int TP = std::min(16, (pairs + device_cus() - 1) / device_cus());
+    const int SK = std::max(1, 16 / TP);
+    const int nl = (G + SK - 1) / SK;
+    if (nl <= 2) return launch_rows16_nl<PAIR, OUT_F32, 2>(x, M, w, s, out, N, K, TP, SK, stream);
+    if (nl <= 4) return launch_rows16_nl<PAIR, OUT_F32, 4>(x, M, w, s, out, N, K, TP, SK, stream);
+    if (nl <= 6) return launch_rows16_nl<PAIR, OUT_F32, 6>(x, M, w, s, out, N, K, TP, SK, stream);
+    if (nl <= 8) return launch_rows16_nl<PAIR, OUT_F32, 8>(x, M, w, s, out, N, K, TP, SK, stream);
+    if (nl <= 12) return launch_rows16_nl<PAIR, OUT_F32, 12>(x, M, w, s, out, N, K, TP, SK, stream);
+    return 1;
+}
+
 template <bool PAIR, bool OUT_F32>
 int launch_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
                 int K, hipStream_t stream) {
+    if (M > 8 && M <= 16) return launch_rows16<PAIR, OUT_F32>(x, M, w, s, out, N, K, stream);
     if (M < 2 || M > 8) return 1;
     const int pairs = (K / 128 + 1) / 2;
     if (pairs <= 12 && M <= 4) {
@@ -1144,6 +1301,21 @@ int launch_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, v
     if (pairs <= 48) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 6>(x, M, w, s, out, N, K, stream);
     if (pairs <= 80) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 10>(x, M, w, s, out, N, K, stream);
     return 1;
+}
+
+/* Compute units of the current device (cached per device; 256 if the query fails). */
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
 }
 
 /* Split-K scratch for the MFMA form: FP32 partials and per-tile-pair arrival counters, one set
@@ -1294,9 +1466,9 @@ int check_gemm_args(const void *a, const void *p, const void *s, const void *o, 
 /* C ABI                                                                                     */
 /* ---------------------------------------------------------------------------------------- */
 
-/* Rows of x: M = 1 takes the v_dot2 GEMV; 2 <= M <= 8 the few-row MFMA kernel where its staged
- * rows fit a block's LDS, otherwise (and for 9 <= M <= 16) the split-K MFMA form, one pass over
- * the weight for all rows; larger M runs on 16-row slices. */
+/* Rows of x: M = 1 takes the v_dot2 GEMV; 2 <= M <= 16 the few-row MFMA kernels where their
+ * staged rows fit a block's LDS, otherwise the split-K MFMA form, one pass over the weight for
+ * all rows; larger M runs on 16-row slices. */
 template <int OUT>
 static int run_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
                     int N, int K, hipStream_t stream) {

@@ -129,12 +129,13 @@ def test_small_m_parity(cuda, m):
     assert_parity(out, oracle.gemm_bf16(x, p, s, n, k), f"gemm M={m}")
 
 
-@pytest.mark.parametrize("m", [2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 6, 7, 8, 9, 12, 16])
 def test_few_rows_parity(cuda, m):
-    """2 <= M <= 8 on the few-row MFMA kernel, through each of its block shapes: 1 group pair,
-    an odd group count with a half-filled block of tiles, 10, 13 (odd) and 38 pairs; the last
-    falls back to the split-K MFMA form once the staged rows pass 64 KiB of LDS (M >= 4). The
-    gate/up pair with the fused SiLU epilogue at an odd group count."""
+    """2 <= M <= 16 on the few-row MFMA kernels, through each of their block shapes: 1 group
+    pair, an odd group count with a half-filled block of tiles (and, from M = 9, a tile pair
+    missing its second tile), 10, 13 (odd) and 38 pairs; the last takes the split-K MFMA form
+    from M = 9 (its staged rows would pass a block's LDS). The gate/up pair with the fused SiLU
+    epilogue at an odd group count."""
     for n, k in [(256, 256), (24, 1152), (2560, 2560), (64, 3200), (640, 9728)]:
         say(f"gemm M={m} n={n} k={k}")
         p, s = make_weight(n, k, seed=n + k + m)
