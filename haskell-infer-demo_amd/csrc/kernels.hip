@@ -51,6 +51,21 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                            __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
+/* Cross-lane moves on the DPP path (a VALU operand modifier, no LDS round trip). quad_perm
+ * patterns permute within groups of four lanes, row_ror:n rotates within rows of sixteen, and
+ * row_half_mirror reverses each group of eight. */
+constexpr int kDppQuadSwap1 = 0xB1;      /* quad_perm [1,0,3,2]: lane ^ 1 */
+constexpr int kDppQuadSwap2 = 0x4E;      /* quad_perm [2,3,0,1]: lane ^ 2 */
+constexpr int kDppRowRor4 = 0x124;       /* row_ror:4 */
+constexpr int kDppRowRor8 = 0x128;       /* row_ror:8: lane ^ 8 within a row */
+constexpr int kDppRowHalfMirror = 0x141; /* lane 7 - l within each group of eight */
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
 /* Code pairs as BF16. In a tile word the pair (j = 2q, 2q+1) sits at bits 4q and 16 + 4q, so one
  * shift puts both nibbles at bits 3-6 of their 16-bit halves and one v_bitop3_b32 computes
  * (s & 0x00780078) ^ 0x3F403F40: it keeps the two nibbles, flips their sign bits (u = code + 8)
@@ -271,9 +286,10 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             s8 += bf16_widen((uint16_t)(w4[q] & 0xFFFFu)) + bf16_widen((uint16_t)(w4[q] >> 16));
-        /* chunk i = 16 g + 4 s + kb: add the four s of one (g, kb) */
-        s8 += __shfl_xor(s8, 4);
-        s8 += __shfl_xor(s8, 8);
+        /* chunk i = 16 g + 4 s + kb (16 consecutive chunks are one DPP row): add the four s
+         * of one (g, kb), i.e. the lanes congruent mod 4 within the row, by two rotations */
+        s8 += dpp_f32<kDppRowRor4>(s8);
+        s8 += dpp_f32<kDppRowRor8>(s8);
         if (i < xchunks && ((i >> 2) & 3) == 0) xsum[(i >> 4) * 4 + (i & 3)] = s8;
     }
     __syncthreads();
@@ -292,7 +308,7 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
     }
 
     /* 5. lanes r, r+8, ..., r+56 hold row r's partials; then the SK waves of a tile */
-    acc += __shfl_xor(acc, 8);
+    acc += dpp_f32<kDppRowRor8>(acc);
     acc += __shfl_xor(acc, 16);
     acc += __shfl_xor(acc, 32);
     float row_sum = acc;
@@ -357,15 +373,18 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
     uint4 *xslice = smem4 + wave * NP * 32; /* pair i: 32 chunks of 16 bytes */
     float *red = reinterpret_cast<float *>(smem4 + SK * NP * 32);
 
-    /* 1. this wave's activation (pair p: values [256 p, 256 p + 256), lane l holds 4 l..4 l+3),
-     * then its weight pieces and scales */
+    /* 1. this wave's activation, then its weight pieces and scales. Pair p holds values
+     * [256 p, 256 p + 256) as 32 chunks of 8; the eight lanes 8 (4 half + kb) + j load the
+     * halves of the chunks c = 16 half + 4 s + kb (s = j >> 1, half j & 1), the 32 values that
+     * the pieces (half, kb, r) of those same lanes multiply. */
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)K * 2);
+    const int xslot = (16 * half + 4 * ((lane & 7) >> 1) + kb) * 2 + (lane & 1); /* 8-byte slot */
     uint2 xv[NP];
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
         const int p = gw + i * kStride;
         const auto v = __builtin_amdgcn_raw_buffer_load_b64(
-            xr, p < P ? (int)(p * 512 + lane * 8) : (int)kOob, 0, 0);
+            xr, p < P ? (int)(p * 512 + xslot * 8) : (int)kOob, 0, 0);
         xv[i] = __builtin_bit_cast(uint2, v);
     }
     const size_t tile_bytes = (size_t)G * 512;
@@ -388,15 +407,13 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
         if (gw + i * kStride < P) { /* wave-uniform */
-            xs2[i * 64 + lane] = xv[i];
-            /* lane l holds chunk c = l / 2 = 16 gl + 4 s + kb of the pair: add the chunk's two
-             * halves (xor 1) and its four s (xor 8, 16); lane 32 gl + 2 kb then holds (gl, kb) */
+            xs2[i * 64 + xslot] = xv[i];
+            /* the (half, kb) sum over the lane's group of eight: three DPP adds */
             float s4 = bf16_widen((uint16_t)(xv[i].x & 0xFFFFu)) + bf16_widen((uint16_t)(xv[i].x >> 16)) +
                        bf16_widen((uint16_t)(xv[i].y & 0xFFFFu)) + bf16_widen((uint16_t)(xv[i].y >> 16));
-            s4 += __shfl_xor(s4, 1);
-            s4 += __shfl_xor(s4, 8);
-            s4 += __shfl_xor(s4, 16);
-            const float xsum = __shfl(s4, 32 * half + 2 * kb);
+            s4 += dpp_f32<kDppQuadSwap1>(s4);
+            s4 += dpp_f32<kDppQuadSwap2>(s4);
+            const float xsum = s4 + dpp_f32<kDppRowHalfMirror>(s4);
             const uint4 *xq = xslice + i * 32 + 16 * half + kb;
             const uint4 xrow[4] = {xq[0], xq[4], xq[8], xq[12]};
             acc = fmaf(piece_dot(buf[i], xrow, xsum), bf16_widen(sbits[i]), acc);
@@ -404,7 +421,7 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
     }
 
     /* 3. lanes r, r+8, ..., r+56 hold row r's partials; then the SK waves of the block */
-    acc += __shfl_xor(acc, 8);
+    acc += dpp_f32<kDppRowRor8>(acc);
     acc += __shfl_xor(acc, 16);
     acc += __shfl_xor(acc, 32);
     if (lane < 8) red[wave * 8 + lane] = acc;
@@ -544,10 +561,10 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
         for (int j = 0; j < 4; ++j)
             s8 += bf16_widen((uint16_t)(w4[j] & 0xFFFFu)) + bf16_widen((uint16_t)(w4[j] >> 16));
         /* 16 consecutive chunks make one group of one row */
-        s8 += __shfl_xor(s8, 1);
-        s8 += __shfl_xor(s8, 2);
-        s8 += __shfl_xor(s8, 4);
-        s8 += __shfl_xor(s8, 8);
+        s8 += dpp_f32<kDppQuadSwap1>(s8);
+        s8 += dpp_f32<kDppQuadSwap2>(s8);
+        s8 += dpp_f32<kDppRowRor4>(s8);
+        s8 += dpp_f32<kDppRowRor8>(s8);
         if (i < chunks && (i & 15) == 0) xsum[i >> 4] = s8;
     };
 #pragma unroll
