@@ -13,7 +13,8 @@
  *
  *   gemv_tiles_kernel   M = 1, block-staged activation (gate/up with the fused SiLU x up
  *                       epilogue, short-K linears); optional RMSNorm (and residual) prologue
- *   gemv_xwave_kernel   M = 1, long K (the down projection): wave-local activation slices;
+ *   gemv_xwave_kernel   M = 1, long K (the down projection) and K = 1792..3072 (with the
+ *                       fused SiLU x up epilogue for gate/up): wave-local activation slices;
  *                       optional residual epilogue
  *   gemv_rows_kernel    2 <= M <= 8: the GEMV's block structure on v_mfma_f32_16x16x32_bf16 with
  *                       a block-diagonal operand, activation loaded straight into LDS
@@ -59,6 +60,7 @@ constexpr int kDppQuadSwap2 = 0x4E;      /* quad_perm [2,3,0,1]: lane ^ 2 */
 constexpr int kDppRowRor4 = 0x124;       /* row_ror:4 */
 constexpr int kDppRowRor8 = 0x128;       /* row_ror:8: lane ^ 8 within a row */
 constexpr int kDppRowHalfMirror = 0x141; /* lane 7 - l within each group of eight */
+constexpr int kDppRowShl4 = 0x104;       /* row_shl:4: lane l reads lane l + 4 of its row */
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
@@ -324,7 +326,7 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
     if (ks != 0 || !tile_ok) return;
     if (PAIR) {
         /* lane r < 4 has gate row r, lane r + 4 the matching up row */
-        const float upv = __shfl_down(row_sum, 4);
+        const float upv = dpp_f32<kDppRowShl4>(row_sum);
         if (lane < 4) {
             const float gate = bf16_widen(bf16_rne(row_sum));
             const float up = bf16_widen(bf16_rne(upv));
@@ -350,7 +352,7 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
  * blocks of a tile store FP32 row partials with agent-scope stores, count on the tile's
  * agent-scope counter, and the last to arrive adds the BS partials in block order (independent
  * of arrival order), writes the row and resets the counter. */
-template <bool OUT_F32, int SK, int NP, int BS>
+template <bool PAIR, bool OUT_F32, int SK, int NP, int BS>
 __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ wt,
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, float *partial,
@@ -449,7 +451,15 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
         if (lane == 0)
             __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (OUT_F32) {
+    if (PAIR) {
+        /* lane r < 4 has gate row r, lane r + 4 the matching up row (lanes 0-7 are active) */
+        const float upv = dpp_f32<kDppRowShl4>(row_sum);
+        if (lane < 4) {
+            const float gate = bf16_widen(bf16_rne(row_sum));
+            const float up = bf16_widen(bf16_rne(upv));
+            reinterpret_cast<uint16_t *>(out)[tile * 4 + lane] = silu_mul_bf16(gate, up);
+        }
+    } else if (OUT_F32) {
         reinterpret_cast<float *>(out)[tile * 8 + lane] = row_sum;
     } else {
         const int row = tile * 8 + lane;
@@ -1151,7 +1161,7 @@ int launch_gemv_cfg(const uint16_t *x, const uint8_t *w, const uint16_t *s, void
 
 int split_scratch(size_t partial_bytes, size_t ncounters, float **partial, unsigned **counters);
 
-template <bool OUT_F32, int NP, int SK, int BS>
+template <bool OUT_F32, int NP, int SK, int BS, bool PAIR = false>
 int launch_xwave_np(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N,
                     int K, hipStream_t stream, uint16_t *residual = nullptr,
                     const uint16_t *sub = nullptr) {
@@ -1162,7 +1172,7 @@ int launch_xwave_np(const uint16_t *x, const uint8_t *w, const uint16_t *s, void
                                &partial, &counters);
         if (st) return st;
     }
-    hipLaunchKernelGGL((gemv_xwave_kernel<OUT_F32, SK, NP, BS>), dim3(N / 8 * BS), dim3(SK * 64),
+    hipLaunchKernelGGL((gemv_xwave_kernel<PAIR, OUT_F32, SK, NP, BS>), dim3(N / 8 * BS), dim3(SK * 64),
                        xwave_smem(SK, NP), stream, x, w, s, out, N, K, partial, counters, residual,
                        sub);
     return hip_status(hipGetLastError(), "gemv launch");
@@ -1197,6 +1207,10 @@ int launch_xwave(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *o
  * - a long K (more group pairs than one wave holds, the down projection) runs the wave-local
  *   activation kernel: at K = 9728 / 8704 / 17408 it takes 5.85 / 8.35 / 12.9 us against
  *   6.2 / 9.7 / 15.7 us for the block-staged kernel;
+ * - 7 to 12 group pairs (K = 1792..3072, the C0/C1 gate/up) run it too, one tile of four waves
+ *   holding three pairs each: C1 gate/up 7.53 against 7.79 us, C0 5.0 against 5.43 (medians of
+ *   interleaved runs; at K = 5120 it only ties the block-staged 1 x 4 x 5, 17.6-17.9 against
+ *   17.4-18.4 us, which stays);
  * - otherwise the block-staged kernel with few loads a wave (NL) and several waves a tile, which
  *   keeps 8 waves a SIMD resident. Medians of 7 interleaved graph runs, whole C1 FFN (gate/up
  *   shape varied, same down kernel): 2 tiles x 2 waves x 5 pairs 13.9 us; 1 x 4 x 3 14.4;
@@ -1210,6 +1224,8 @@ int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *ou
         const int st = launch_xwave<OUT_F32>(x, w, s, out, N, K, stream);
         if (st <= 0) return st;
     }
+    if (!norm && pairs > 6 && pairs <= 12)
+        return launch_xwave_np<OUT_F32, 3, 4, 1, PAIR>(x, w, s, out, N, K, stream);
     if (norm) {
         /* every block normalises all of x, yet the small-load shape still wins over fewer,
          * larger blocks (C1 norm + FFN medians: 2 x 2 x 5 14.9 us, 4 x 1 x 10 15.4, 4 x 2 x 5

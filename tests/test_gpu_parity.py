@@ -105,7 +105,10 @@ def test_quantize_device_bit_exact(cuda):
                                  # the reference's M = 1 limit (K * 2 = 96 KiB): 8 blocks a tile
                                  (64, 49152),
                                  # wave-local kernel, one pair a wave, 288 and 384 tiles
-                                 (2304, 4096), (3072, 4096)])
+                                 (2304, 4096), (3072, 4096),
+                                 # 7 to 12 group pairs: four waves of three pairs a tile,
+                                 # including odd group counts
+                                 (64, 1792), (64, 2816), (40, 3072), (16, 2944), (56, 1920)])
 def test_gemv_parity(cuda, n, k):
     say(f"gemv n={n} k={k}")
     p, s = make_weight(n, k, seed=n + k)
@@ -213,16 +216,19 @@ def test_silu_mul_packed(cuda):
     assert np.array_equal(host, got)
 
 
-def test_gate_up_silu_parity(cuda):
-    hidden, inter = 2560, 9728
-    say("gate_up_silu C1")
-    gup, gus, _, _ = make_ffn(hidden, inter)
+@pytest.mark.parametrize("hidden,inter", [(2560, 9728), (1920, 200), (1152, 72), (3072, 40),
+                                          (5120, 64)])
+def test_gate_up_silu_parity(cuda, hidden, inter):
+    """The fused gate/up/SiLU at M = 1 on each of its kernels: C1 and odd group counts on the
+    wave-local kernel (8 and 12 pairs), the block-staged one below and above (5 and 20 pairs)."""
+    say(f"gate_up_silu H={hidden} I={inter}")
+    gup, gus = make_weight(2 * inter, hidden, seed=hidden + inter)
     x = oracle.synth_activation(1, hidden, seed=7)
     gu = w4a16.TiledWeight.from_artifact(gup, gus, 2 * inter, hidden, pair=True, device=cuda)
     act = from_dev(w4a16.gate_up_silu(to_dev(x, cuda), gu))
     mid = oracle.gemm_bf16(x, gup, gus, 2 * inter, hidden)
     want = oracle.silu_mul_packed(mid, 1, inter)
-    assert_parity(act, want, "gate_up_silu C1")
+    assert_parity(act, want, f"gate_up_silu H={hidden} I={inter}")
 
 
 @pytest.mark.parametrize("hidden,inter,m", [(2560, 9728, 1), (5120, 17408, 1), (2560, 9728, 2),
