@@ -262,7 +262,10 @@ def main():
 
             f2_us, _, _ = timed(capture(f2_call), args.steps, args.warmup)
     args.steps = calls
-    family = ("gemv_tiles_kernel" if m == 1 else "gemv_rows_kernel" if m <= 8
+    # the kernel the library routes the dominant launch to (gate/up, or the linear of config 0)
+    hidden_pairs = (hidden // 128 + 1) // 2
+    m1_family = "gemv_xwave_kernel" if 6 < hidden_pairs <= 12 else "gemv_tiles_kernel"
+    family = (m1_family if m == 1 else "gemv_rows_kernel" if m <= 8
               else "gemv_rows16_kernel" if m <= 16 else "mfma_gemm_kernel")
     if linear_only:
         dom_bytes = per_set
