@@ -99,9 +99,10 @@ def test_quantize_device_bit_exact(cuda):
 
 @pytest.mark.parametrize("n,k", [(9728, 2560), (2560, 9728), (5120, 17408), (8704, 5120),
                                  (256, 128), (1024, 384), (24, 1152),
-                                 # wave-local kernel with an odd group count (13 pairs, NP = 1),
-                                 # its widest slice (NP = 7), and past it (block-staged, SK = 16)
-                                 (64, 3200), (40, 28672), (16, 30464),
+                                 # wave-local kernel: an odd group count (13 pairs, one a
+                                 # wave), tiles split over three and four blocks (64 and 96
+                                 # pairs) and over five (112 and 119 pairs)
+                                 (64, 3200), (64, 16384), (32, 24576), (40, 28672), (16, 30464),
                                  # the reference's M = 1 limit (K * 2 = 96 KiB): 8 blocks a tile
                                  (64, 49152),
                                  # wave-local kernel, one pair a wave, 288 and 384 tiles
