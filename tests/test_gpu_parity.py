@@ -321,6 +321,38 @@ def test_ffn_norm_parity(cuda, style, m):
     assert rel <= 1e-3, rel
 
 
+@pytest.mark.parametrize("hidden", [1152, 1920, 3072])
+def test_norm_prologue_shapes(cuda, hidden):
+    """The M = 1 norm (and plan-F2) prologue of the block-staged gate/up kernel at 5, 8 (odd
+    group count) and 12 group pairs: the act stage and the F2 layer output against the oracle,
+    the updated residual bit-exact given the kernel's output."""
+    import torch
+
+    inter = 128
+    say(f"norm prologue H={hidden}")
+    gup, gus = make_weight(2 * inter, hidden, seed=500 + hidden)
+    dp, ds = make_weight(hidden, inter, seed=600 + hidden)
+    gu = w4a16.TiledWeight.from_artifact(gup, gus, 2 * inter, hidden, pair=True, device=cuda)
+    dn = w4a16.TiledWeight.from_artifact(dp, ds, hidden, inter, device=cuda)
+    for style in (0, 1):
+        x, w = norm_inputs(1, hidden, style, seed=70 + hidden)
+        xd = to_dev(x, cuda)
+        ws = torch.empty((1, hidden + inter), dtype=xd.dtype, device=cuda)
+        w4a16.mlp_int4_norm(xd, to_dev(w, cuda), style, 1e-6, gu, dn, ws=ws)
+        act = from_dev(ws.reshape(-1)[hidden:].reshape(1, inter))
+        _, _, ref_act = oracle.ffn_bf16(oracle.rmsnorm_bf16(x, w, style, 1e-6), gup, gus, dp, ds,
+                                        hidden, inter)
+        assert_parity(act, ref_act, f"norm prologue H={hidden} style={style}", floor_div=16.0)
+        sub = oracle.synth_activation(1, hidden, seed=71 + hidden)
+        r_mid, normed = oracle.residual_norm_bf16(x, sub, w, style, 1e-6)
+        ref, _, _ = oracle.ffn_bf16(normed, gup, gus, dp, ds, hidden, inter)
+        res = to_dev(x, cuda)
+        got = from_dev(w4a16.mlp_int4_residual_norm(res, to_dev(sub, cuda), to_dev(w, cuda),
+                                                    style, 1e-6, gu, dn))
+        assert_parity(got, ref, f"F2 H={hidden} style={style}", floor_div=16.0)
+        assert np.array_equal(from_dev(res), oracle.residual_add_bf16(r_mid, got))
+
+
 @pytest.mark.parametrize("style", [0, 1])
 @pytest.mark.parametrize("m", [1, 2, 16])
 def test_ffn_residual_norm_parity(cuda, style, m):
