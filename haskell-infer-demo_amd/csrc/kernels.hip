@@ -9,7 +9,8 @@
  * a piece's contribution is 32 * dot(v, x) - 24 * sum(x), with the per-piece activation sums
  * formed once when the activation is staged in LDS. The group's BF16 scale multiplies each
  * piece's FP32 partial (the association of the reference's tiled kernel,
- * csrc/kernels/gemm_quant.cu:130-142). Lanes of one row are reduced with cross-lane shuffles.
+ * csrc/kernels/gemm_quant.cu:130-142). Lanes of one row are reduced with DPP moves within rows
+ * of 16 lanes and shuffles across them.
  *
  *   gemv_tiles_kernel   M = 1, block-staged activation (gate/up with the fused SiLU x up
  *                       epilogue, short-K linears); optional RMSNorm (and residual) prologue
@@ -1236,8 +1237,6 @@ int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *ou
     }
     if (pairs <= 3) return launch_gemv_cfg<PAIR, OUT_F32, 4, 1, 3>(x, w, s, out, N, K, stream);
     if (pairs <= 6) return launch_gemv_cfg<PAIR, OUT_F32, 2, 2, 3>(x, w, s, out, N, K, stream);
-    if (pairs <= 10) return launch_gemv_cfg<PAIR, OUT_F32, 2, 2, 5>(x, w, s, out, N, K, stream);
-    if (pairs <= 12) return launch_gemv_cfg<PAIR, OUT_F32, 2, 2, 6>(x, w, s, out, N, K, stream);
     if (pairs <= 20) return launch_gemv_cfg<PAIR, OUT_F32, 1, 4, 5>(x, w, s, out, N, K, stream);
     if (pairs <= 48) return launch_gemv_cfg<PAIR, OUT_F32, 1, 8, 6>(x, w, s, out, N, K, stream);
     if (pairs <= 96) return launch_gemv_cfg<PAIR, OUT_F32, 1, 16, 6>(x, w, s, out, N, K, stream);
