@@ -712,10 +712,11 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
  * the 16 lanes of one ds_read_b128 pass (one k block, rows 8a + m) then read 16 consecutive
  * chunks, which covers every bank once. Chunks of a group past K are loaded as zeros.
  * ---------------------------------------------------------------------------------------- */
-template <bool PAIR, bool OUT_F32, int TB, int SK, int NL, int MI>
+template <bool PAIR, bool OUT_F32, int TB, int SK, int NL, int MI, bool NORM = false>
 __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
     const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
-    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K) {
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K,
+    const uint16_t *__restrict__ norm_w, float norm_bias, float eps) {
     constexpr int W = TB * SK;
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
@@ -725,6 +726,8 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
     const int nlds = P * 32 * M;        /* staged chunks (both groups of every pair) */
     const int nins = (nlds + 63) >> 6;  /* 1 KiB load instructions */
     float *red = reinterpret_cast<float *>(smem4 + nins * 64); /* [W][8 rows][8 tile rows] */
+    uint4 *wl = reinterpret_cast<uint4 *>(red + W * 64);       /* NORM: the norm weight [K] */
+    float *rms = reinterpret_cast<float *>(wl + (NORM ? ((K >> 3) + 63) / 64 * 64 : 0));
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -751,6 +754,15 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
             xr, (__attribute__((address_space(3))) void *)(smem4 + j * 64), 16, off, 0, 0, 0);
         ++xloads;
     }
+    if (NORM) { /* the norm weight, [K] in order, the same way */
+        const __amdgpu_buffer_rsrc_t nr = make_rsrc(norm_w, (uint32_t)K * 2);
+        for (int j = wave; j < ((K >> 3) + 63) / 64; j += W) {
+            const int c = j * 64 + lane;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                nr, (__attribute__((address_space(3))) void *)(wl + j * 64), 16,
+                c < (K >> 3) ? (uint32_t)c * 16 : kOob, 0, 0, 0);
+        }
+    }
 
     /* 2. every weight piece and scale of this wave */
     const bool tile_ok = tile < tiles;
@@ -775,6 +787,60 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
     (void)xloads;
     __builtin_amdgcn_s_waitcnt(kVmcntWeights<NL>);
     __syncthreads();
+
+    /* 3b. NORM: each staged row becomes its RMSNorm, BF16(x * rsqrt(sum x^2 / K + eps) *
+     * (norm_bias + w)) in the FP32 order of the reference's norm (FlashInfer RMSNorm /
+     * GemmaRMSNorm behind csrc/kernels/flashinfer_norm.cu:22-76). Wave m sums row m's squares
+     * (a fixed order: per lane, then DPP within rows of 16 and shuffles across them; W >= M for
+     * every launch with NORM), then every thread normalises its staged chunks in place. The
+     * weight loads issued above keep streaming meanwhile. */
+    if (NORM) {
+        if (wave < M) {
+            float ss = 0.0f;
+            for (int j = lane; j < P * 32; j += 64) { /* row m's chunks: (pair, chunk, a) */
+                const int pp = j >> 5, c = (j >> 1) & 15, aa = j & 1;
+                const uint4 ch = smem4[(pp * 16 + c) * 2 * M + 2 * wave + aa];
+                const uint32_t w4[4] = {ch.x, ch.y, ch.z, ch.w};
+#pragma unroll
+                for (int q2 = 0; q2 < 4; ++q2) {
+                    const float lo = bf16_widen((uint16_t)(w4[q2] & 0xFFFFu));
+                    const float hi = bf16_widen((uint16_t)(w4[q2] >> 16));
+                    ss = fmaf(lo, lo, ss);
+                    ss = fmaf(hi, hi, ss);
+                }
+            }
+            ss += dpp_f32<kDppQuadSwap1>(ss);
+            ss += dpp_f32<kDppQuadSwap2>(ss);
+            ss += dpp_f32<kDppRowRor4>(ss);
+            ss += dpp_f32<kDppRowRor8>(ss);
+            ss += __shfl_xor(ss, 16);
+            ss += __shfl_xor(ss, 32);
+            if (lane == 0) rms[wave] = 1.0f / sqrtf(ss / (float)K + eps);
+        }
+        __syncthreads();
+        for (int pos = tid; pos < nlds; pos += W * 64) {
+            const int t2 = pos >> 1;
+            const int m = t2 % M, t3 = t2 / M;
+            const int g = 2 * (t3 >> 4) + (pos & 1), c = t3 & 15;
+            if (g >= G) continue; /* a staged group past K is zero and stays zero */
+            const float rm = rms[m];
+            const uint4 v = smem4[pos];
+            const uint4 wv = wl[g * 16 + c];
+            uint32_t x4[4] = {v.x, v.y, v.z, v.w};
+            const uint32_t n4[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int q2 = 0; q2 < 4; ++q2) {
+                const float lo = bf16_widen((uint16_t)(x4[q2] & 0xFFFFu)) * rm *
+                                 (norm_bias + bf16_widen((uint16_t)(n4[q2] & 0xFFFFu)));
+                const float hi = bf16_widen((uint16_t)(x4[q2] >> 16)) * rm *
+                                 (norm_bias + bf16_widen((uint16_t)(n4[q2] >> 16)));
+                const bf16x2_t packed = {(__bf16)lo, (__bf16)hi};
+                x4[q2] = __builtin_bit_cast(uint32_t, packed);
+            }
+            smem4[pos] = make_uint4(x4[0], x4[1], x4[2], x4[3]);
+        }
+        __syncthreads();
+    }
 
     /* 4. eight MFMAs a pair. A piece past the tile's groups has scale 0 (its loads read 0) and
      * its staged activation is zero, so it adds exactly 0 without a branch; lanes of A rows
@@ -1245,23 +1311,33 @@ int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *ou
 
 /* Few-row kernel: LDS for both groups of every pair of the M rows (whole 1 KiB load
  * instructions) and the wave reduction. */
-size_t rows_smem(int M, int K, int waves) {
+size_t rows_smem(int M, int K, int waves, bool norm = false) {
     const int P = (K / 128 + 1) / 2;
-    return (size_t)((P * 32 * M + 63) / 64) * 1024 + (size_t)waves * 256;
+    return (size_t)((P * 32 * M + 63) / 64) * 1024 + (size_t)waves * 256 +
+           (norm ? (size_t)((K / 8 + 63) / 64) * 1024 + 32 : 0);
 }
 
 template <bool PAIR, bool OUT_F32, int TB, int SK, int NL>
 int launch_rows_mi(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
-                   int N, int K, hipStream_t stream) {
-    const size_t smem = rows_smem(M, K, TB * SK);
+                   int N, int K, hipStream_t stream, const NormArgs *norm = nullptr) {
+    const size_t smem = rows_smem(M, K, TB * SK, norm != nullptr);
     if (smem > kMaxLds) return 1;
+    if (norm && TB * SK < M) return 1; /* the prologue gives each row a wave */
     const dim3 grid((N / 8 + TB - 1) / TB), block(TB * SK * 64);
-    if (M == 2)
+    const uint16_t *nw = norm ? norm->w : nullptr;
+    const float nb = norm ? norm->bias : 0.0f, ne = norm ? norm->eps : 0.0f;
+    if (M == 2 && norm)
+        hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 2, true>), grid, block,
+                           smem, stream, x, M, w, s, out, N, K, nw, nb, ne);
+    else if (M == 2)
         hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 2>), grid, block, smem,
-                           stream, x, M, w, s, out, N, K);
+                           stream, x, M, w, s, out, N, K, nw, nb, ne);
+    else if (norm)
+        hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 4, true>), grid, block,
+                           smem, stream, x, M, w, s, out, N, K, nw, nb, ne);
     else
         hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 4>), grid, block, smem,
-                           stream, x, M, w, s, out, N, K);
+                           stream, x, M, w, s, out, N, K, nw, nb, ne);
     return hip_status(hipGetLastError(), "gemv rows launch");
 }
 
@@ -1312,26 +1388,27 @@ int launch_rows16(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s,
 
 template <bool PAIR, bool OUT_F32>
 int launch_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
-                int K, hipStream_t stream) {
-    if (M > 8 && M <= 16) return launch_rows16<PAIR, OUT_F32>(x, M, w, s, out, N, K, stream);
+                int K, hipStream_t stream, const NormArgs *norm = nullptr) {
+    if (M > 8 && M <= 16 && !norm)
+        return launch_rows16<PAIR, OUT_F32>(x, M, w, s, out, N, K, stream);
     if (M < 2 || M > 8) return 1;
     const int pairs = (K / 128 + 1) / 2;
     if (pairs <= 12 && M <= 4) {
-        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 4, 1, 3>(x, M, w, s, out, N, K, stream);
-        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 3>(x, M, w, s, out, N, K, stream);
-        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 5>(x, M, w, s, out, N, K, stream);
-        return launch_rows_mi<PAIR, OUT_F32, 2, 2, 6>(x, M, w, s, out, N, K, stream);
+        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 4, 1, 3>(x, M, w, s, out, N, K, stream, norm);
+        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 3>(x, M, w, s, out, N, K, stream, norm);
+        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 5>(x, M, w, s, out, N, K, stream, norm);
+        return launch_rows_mi<PAIR, OUT_F32, 2, 2, 6>(x, M, w, s, out, N, K, stream, norm);
     }
     if (pairs <= 12) {
-        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 8, 1, 3>(x, M, w, s, out, N, K, stream);
-        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 3>(x, M, w, s, out, N, K, stream);
-        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 5>(x, M, w, s, out, N, K, stream);
-        return launch_rows_mi<PAIR, OUT_F32, 4, 2, 6>(x, M, w, s, out, N, K, stream);
+        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 8, 1, 3>(x, M, w, s, out, N, K, stream, norm);
+        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 3>(x, M, w, s, out, N, K, stream, norm);
+        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 5>(x, M, w, s, out, N, K, stream, norm);
+        return launch_rows_mi<PAIR, OUT_F32, 4, 2, 6>(x, M, w, s, out, N, K, stream, norm);
     }
-    if (pairs <= 20) return launch_rows_mi<PAIR, OUT_F32, 2, 4, 5>(x, M, w, s, out, N, K, stream);
-    if (pairs <= 40) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 5>(x, M, w, s, out, N, K, stream);
-    if (pairs <= 48) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 6>(x, M, w, s, out, N, K, stream);
-    if (pairs <= 80) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 10>(x, M, w, s, out, N, K, stream);
+    if (pairs <= 20) return launch_rows_mi<PAIR, OUT_F32, 2, 4, 5>(x, M, w, s, out, N, K, stream, norm);
+    if (pairs <= 40) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 5>(x, M, w, s, out, N, K, stream, norm);
+    if (pairs <= 48) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 6>(x, M, w, s, out, N, K, stream, norm);
+    if (pairs <= 80) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 10>(x, M, w, s, out, N, K, stream, norm);
     return 1;
 }
 
@@ -1634,9 +1711,14 @@ static int mlp_norm_common(const uint16_t *residual, const uint16_t *norm_w, int
      * while a block's waves each hold all of K (measured at H = 2560: 16.2 us per norm + FFN
      * call fused, 17.8 us with a separate norm launch); at H = 5120 the separate launch is
      * cheaper (35.0 against 38.4 us). */
-    if (M == 1 && (hidden / W4A16_GROUP + 1) / 2 <= kMaxLoads) {
+    st = 1;
+    if (M == 1 && (hidden / W4A16_GROUP + 1) / 2 <= kMaxLoads)
         st = launch_gemv<true, false>(residual, gup, gus, act, 2 * inter, hidden, s, &na);
-    } else {
+    else if (M == 2) /* the few-row kernel's own prologue (C3 norm + FFN: M = 2 18.1-18.4 us
+                      * against 19.2 with the separate norm; M = 4 21.5 against 20.4-20.9 and
+                      * M = 8 26.2-26.7 against 24.0, every block normalising all M rows) */
+        st = launch_rows<true, false>(residual, M, gup, gus, act, 2 * inter, hidden, s, &na);
+    if (st > 0) {
         st = launch_rmsnorm(normed, residual, norm_w, hidden, M, na.bias, eps, s);
         if (!st) st = run_rows<kOutPairSilu>(normed, M, gup, gus, act, 2 * inter, hidden, s);
     }

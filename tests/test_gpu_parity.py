@@ -296,9 +296,10 @@ def test_rmsnorm_parity(cuda, style):
 @pytest.mark.parametrize("m", [1, 2, 16])
 def test_ffn_norm_parity(cuda, style, m):
     """mlp_int4_norm (forward_mlp, reference csrc/kernels/layers.cu:150-159) against the
-    oracle's RMSNorm followed by the oracle FFN, at the end-to-end bar of test_ffn_parity; at
-    M = 1 the norm runs inside the gate/up kernel, at M > 1 in its own kernel ahead of the MFMA
-    form. The FP32 partial form is checked against the oracle's unrounded partial."""
+    oracle's RMSNorm followed by the oracle FFN, at the end-to-end bar of test_ffn_parity; up to
+    M = 8 the norm runs inside the gate/up kernel (the GEMV's or the few-row kernel's prologue),
+    at M = 16 in its own kernel ahead of the MFMA kernels. The FP32 partial form is checked
+    against the oracle's unrounded partial."""
     hidden, inter = 2560, 9728
     say(f"ffn norm style={style} M={m}")
     gup, gus, dp, ds = make_ffn(hidden, inter)
@@ -319,6 +320,37 @@ def test_ffn_norm_parity(cuda, style, m):
     want = oracle.ffn_partial_f32(normed, gup, gus, dp, ds, hidden, inter)
     rel = np.linalg.norm(part.astype(np.float64) - want) / np.linalg.norm(want)
     assert rel <= 1e-3, rel
+
+
+@pytest.mark.parametrize("m", [2, 3, 5, 8])
+def test_ffn_norm_fused_rows(cuda, m):
+    """mlp_int4_norm for 2 <= M <= 8 (the few-row kernel's own norm prologue at M = 2, the
+    standalone RMSNorm ahead of it from M = 3) against the explicit composition, the standalone
+    RMSNorm then the fused gate/up: bit-identical act and output, for both norm styles; and
+    within rel-L2 1e-3 of the oracle. (Against the oracle's per-element bar these residual
+    inputs leave a few act values at 3 BF16 ULP at M = 5 and 8 on either path, from the FP32
+    norm's rounding of values that sit on a BF16 boundary.)"""
+    import torch
+
+    hidden, inter = 2560, 9728
+    say(f"ffn fused-rows norm M={m}")
+    gup, gus, dp, ds = make_ffn(hidden, inter)
+    gu = w4a16.TiledWeight.from_artifact(gup, gus, 2 * inter, hidden, pair=True, device=cuda)
+    dn = w4a16.TiledWeight.from_artifact(dp, ds, hidden, inter, device=cuda)
+    for style in (0, 1):
+        x, w = norm_inputs(m, hidden, style, seed=60 + m)
+        xd, wd = to_dev(x, cuda), to_dev(w, cuda)
+        ws = torch.empty((m, hidden + inter), dtype=xd.dtype, device=cuda)
+        out = from_dev(w4a16.mlp_int4_norm(xd, wd, style, 1e-6, gu, dn, ws=ws))
+        act = from_dev(ws.reshape(-1)[m * hidden:].reshape(m, inter))
+        normed = w4a16.rmsnorm(xd, wd, style, 1e-6)
+        act2 = w4a16.gate_up_silu(normed, gu)
+        assert np.array_equal(act, from_dev(act2)), (m, style)
+        assert np.array_equal(out, from_dev(w4a16.gemm_int4_bf16(act2, dn))), (m, style)
+        ref, _, _ = oracle.ffn_bf16(oracle.rmsnorm_bf16(x, w, style, 1e-6), gup, gus, dp, ds,
+                                    hidden, inter)
+        o, r = bf16_f32(out).astype(np.float64), bf16_f32(ref).astype(np.float64)
+        assert np.linalg.norm(o - r) / np.linalg.norm(r) <= 1e-3, (m, style)
 
 
 @pytest.mark.parametrize("hidden", [1152, 1920, 3072])
