@@ -468,8 +468,10 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
         if (residual) {
             /* plan F2 epilogue: residual <- BF16(BF16(residual + sub) + out), the updates of
              * reference csrc/layer_dispatch.cu:193-209 (this row's inputs are read before
-             * its output is written, so sub may alias out) */
-            const uint16_t rsum = (uint16_t)(bf16_add2(residual[row], sub[row]) & 0xFFFFu);
+             * its output is written, so sub may alias out); with no sub the residual already
+             * holds BF16(residual + sub) and only the second update is made */
+            const uint16_t rsum =
+                sub ? (uint16_t)(bf16_add2(residual[row], sub[row]) & 0xFFFFu) : residual[row];
             residual[row] = (uint16_t)(bf16_add2(rsum, o) & 0xFFFFu);
         }
         reinterpret_cast<uint16_t *>(out)[row] = o;
@@ -1784,7 +1786,13 @@ extern "C" int mlp_int4_residual_norm_bf16(uint16_t *residual, const uint16_t *s
     }
     st = launch_rmsnorm(normed, residual, norm_w, hidden, M, na.bias, eps, s, sublayer);
     if (!st) st = run_rows<kOutPairSilu>(normed, M, gup, gus, act, 2 * inter, hidden, s);
-    if (!st) st = run_rows<kOutBf16>(act, M, dnp, dns, out, hidden, inter, s);
+    if (st) return st;
+    if (M == 1 && dn_pairs > kMaxLoads) {
+        /* the down kernel adds the output into the (already updated) residual itself */
+        st = launch_xwave<false>(act, dnp, dns, out, hidden, inter, s, residual, nullptr);
+        if (st <= 0) return st;
+    }
+    st = run_rows<kOutBf16>(act, M, dnp, dns, out, hidden, inter, s);
     if (st) return st;
     const long long chunks = (long long)M * hidden / 8;
     hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, s,

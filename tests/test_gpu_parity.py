@@ -353,6 +353,28 @@ def test_ffn_norm_fused_rows(cuda, m):
         assert np.linalg.norm(o - r) / np.linalg.norm(r) <= 1e-3, (m, style)
 
 
+def test_f2_separate_norm_m1(cuda):
+    """Plan F2 at M = 1 past the fused prologue's hidden size (13 group pairs): the standalone
+    norm updates the residual, and the down kernel adds its output into it (no sublayer in its
+    epilogue); the layer output against the oracle and the residual bit-exact given it."""
+    hidden, inter = 3328, 3328
+    say(f"F2 separate norm H={hidden} I={inter}")
+    gup, gus = make_weight(2 * inter, hidden, seed=700)
+    dp, ds = make_weight(hidden, inter, seed=701)
+    gu = w4a16.TiledWeight.from_artifact(gup, gus, 2 * inter, hidden, pair=True, device=cuda)
+    dn = w4a16.TiledWeight.from_artifact(dp, ds, hidden, inter, device=cuda)
+    for style in (0, 1):
+        x, w = norm_inputs(1, hidden, style, seed=72)
+        sub = oracle.synth_activation(1, hidden, seed=73)
+        r_mid, normed = oracle.residual_norm_bf16(x, sub, w, style, 1e-6)
+        ref, _, _ = oracle.ffn_bf16(normed, gup, gus, dp, ds, hidden, inter)
+        res = to_dev(x, cuda)
+        got = from_dev(w4a16.mlp_int4_residual_norm(res, to_dev(sub, cuda), to_dev(w, cuda),
+                                                    style, 1e-6, gu, dn))
+        assert_parity(got, ref, f"F2 H={hidden} style={style}", floor_div=16.0)
+        assert np.array_equal(from_dev(res), oracle.residual_add_bf16(r_mid, got))
+
+
 @pytest.mark.parametrize("hidden", [1152, 1920, 3072])
 def test_norm_prologue_shapes(cuda, hidden):
     """The M = 1 norm (and plan-F2) prologue of the block-staged gate/up kernel at 5, 8 (odd
