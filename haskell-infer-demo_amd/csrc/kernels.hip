@@ -518,7 +518,7 @@ template <int OUT, int XPRE, int MI>
 __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
     const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, int S, int GS,
-    float *__restrict__ partial, unsigned *__restrict__ counters) {
+    float *__restrict__ partial, unsigned *__restrict__ counters, uint16_t *residual) {
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
     const int tiles = N >> 3;
@@ -687,10 +687,14 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
             const int m = 4 * q + i;
             if (m < M && tile < tiles) {
                 const size_t o = (size_t)m * N + tile * 8 + r;
-                if (OUT == kOutF32)
+                if (OUT == kOutF32) {
                     reinterpret_cast<float *>(out)[o] = acc[i];
-                else
-                    reinterpret_cast<uint16_t *>(out)[o] = bf16_rne(acc[i]);
+                } else {
+                    const uint16_t ob = bf16_rne(acc[i]);
+                    /* plan F2: the residual, already BF16(residual + sublayer), gains the output */
+                    if (residual) residual[o] = (uint16_t)(bf16_add2(residual[o], ob) & 0xFFFFu);
+                    reinterpret_cast<uint16_t *>(out)[o] = ob;
+                }
             }
         }
     }
@@ -718,7 +722,7 @@ template <bool PAIR, bool OUT_F32, int TB, int SK, int NL, int MI, bool NORM = f
 __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
     const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K,
-    const uint16_t *__restrict__ norm_w, float norm_bias, float eps) {
+    const uint16_t *__restrict__ norm_w, float norm_bias, float eps, uint16_t *residual) {
     constexpr int W = TB * SK;
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
@@ -895,10 +899,14 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
         }
     } else if (m < M) {
         const size_t o = (size_t)m * N + tile * 8 + r;
-        if (OUT_F32)
+        if (OUT_F32) {
             reinterpret_cast<float *>(out)[o] = row_sum;
-        else
-            reinterpret_cast<uint16_t *>(out)[o] = bf16_rne(row_sum);
+        } else {
+            const uint16_t ob = bf16_rne(row_sum);
+            /* plan F2: the residual, already BF16(residual + sublayer), gains the output */
+            if (residual) residual[o] = (uint16_t)(bf16_add2(residual[o], ob) & 0xFFFFu);
+            reinterpret_cast<uint16_t *>(out)[o] = ob;
+        }
     }
 }
 
@@ -1321,7 +1329,8 @@ size_t rows_smem(int M, int K, int waves, bool norm = false) {
 
 template <bool PAIR, bool OUT_F32, int TB, int SK, int NL>
 int launch_rows_mi(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
-                   int N, int K, hipStream_t stream, const NormArgs *norm = nullptr) {
+                   int N, int K, hipStream_t stream, const NormArgs *norm = nullptr,
+                   uint16_t *residual = nullptr) {
     const size_t smem = rows_smem(M, K, TB * SK, norm != nullptr);
     if (smem > kMaxLds) return 1;
     if (norm && TB * SK < M) return 1; /* the prologue gives each row a wave */
@@ -1330,16 +1339,16 @@ int launch_rows_mi(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s
     const float nb = norm ? norm->bias : 0.0f, ne = norm ? norm->eps : 0.0f;
     if (M == 2 && norm)
         hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 2, true>), grid, block,
-                           smem, stream, x, M, w, s, out, N, K, nw, nb, ne);
+                           smem, stream, x, M, w, s, out, N, K, nw, nb, ne, residual);
     else if (M == 2)
         hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 2>), grid, block, smem,
-                           stream, x, M, w, s, out, N, K, nw, nb, ne);
+                           stream, x, M, w, s, out, N, K, nw, nb, ne, residual);
     else if (norm)
         hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 4, true>), grid, block,
-                           smem, stream, x, M, w, s, out, N, K, nw, nb, ne);
+                           smem, stream, x, M, w, s, out, N, K, nw, nb, ne, residual);
     else
         hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 4>), grid, block, smem,
-                           stream, x, M, w, s, out, N, K, nw, nb, ne);
+                           stream, x, M, w, s, out, N, K, nw, nb, ne, residual);
     return hip_status(hipGetLastError(), "gemv rows launch");
 }
 
@@ -1390,27 +1399,28 @@ int launch_rows16(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s,
 
 template <bool PAIR, bool OUT_F32>
 int launch_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
-                int K, hipStream_t stream, const NormArgs *norm = nullptr) {
-    if (M > 8 && M <= 16 && !norm)
+                int K, hipStream_t stream, const NormArgs *norm = nullptr,
+                uint16_t *residual = nullptr) {
+    if (M > 8 && M <= 16 && !norm && !residual)
         return launch_rows16<PAIR, OUT_F32>(x, M, w, s, out, N, K, stream);
     if (M < 2 || M > 8) return 1;
     const int pairs = (K / 128 + 1) / 2;
     if (pairs <= 12 && M <= 4) {
-        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 4, 1, 3>(x, M, w, s, out, N, K, stream, norm);
-        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 3>(x, M, w, s, out, N, K, stream, norm);
-        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 5>(x, M, w, s, out, N, K, stream, norm);
-        return launch_rows_mi<PAIR, OUT_F32, 2, 2, 6>(x, M, w, s, out, N, K, stream, norm);
+        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 4, 1, 3>(x, M, w, s, out, N, K, stream, norm, residual);
+        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 3>(x, M, w, s, out, N, K, stream, norm, residual);
+        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 5>(x, M, w, s, out, N, K, stream, norm, residual);
+        return launch_rows_mi<PAIR, OUT_F32, 2, 2, 6>(x, M, w, s, out, N, K, stream, norm, residual);
     }
     if (pairs <= 12) {
-        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 8, 1, 3>(x, M, w, s, out, N, K, stream, norm);
-        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 3>(x, M, w, s, out, N, K, stream, norm);
-        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 5>(x, M, w, s, out, N, K, stream, norm);
-        return launch_rows_mi<PAIR, OUT_F32, 4, 2, 6>(x, M, w, s, out, N, K, stream, norm);
+        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 8, 1, 3>(x, M, w, s, out, N, K, stream, norm, residual);
+        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 3>(x, M, w, s, out, N, K, stream, norm, residual);
+        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 5>(x, M, w, s, out, N, K, stream, norm, residual);
+        return launch_rows_mi<PAIR, OUT_F32, 4, 2, 6>(x, M, w, s, out, N, K, stream, norm, residual);
     }
-    if (pairs <= 20) return launch_rows_mi<PAIR, OUT_F32, 2, 4, 5>(x, M, w, s, out, N, K, stream, norm);
-    if (pairs <= 40) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 5>(x, M, w, s, out, N, K, stream, norm);
-    if (pairs <= 48) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 6>(x, M, w, s, out, N, K, stream, norm);
-    if (pairs <= 80) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 10>(x, M, w, s, out, N, K, stream, norm);
+    if (pairs <= 20) return launch_rows_mi<PAIR, OUT_F32, 2, 4, 5>(x, M, w, s, out, N, K, stream, norm, residual);
+    if (pairs <= 40) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 5>(x, M, w, s, out, N, K, stream, norm, residual);
+    if (pairs <= 48) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 6>(x, M, w, s, out, N, K, stream, norm, residual);
+    if (pairs <= 80) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 10>(x, M, w, s, out, N, K, stream, norm, residual);
     return 1;
 }
 
@@ -1507,23 +1517,26 @@ MfmaPlan plan_mfma(int M, int N, int K) {
 template <int OUT, int XPRE>
 int launch_mfma_x(const MfmaPlan &p, const uint16_t *x, int M, const uint8_t *w,
                   const uint16_t *s, void *out, int N, int K, float *partial, unsigned *counters,
-                  hipStream_t stream) {
+                  hipStream_t stream, uint16_t *residual) {
     if (M == 1)
         hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE, 1>), dim3(p.grid), dim3(kMfmaWaves * 64),
-                           p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters);
+                           p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters,
+                           residual);
     else if (M == 2)
         hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE, 2>), dim3(p.grid), dim3(kMfmaWaves * 64),
-                           p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters);
+                           p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters,
+                           residual);
     else
         hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE, 4>), dim3(p.grid), dim3(kMfmaWaves * 64),
-                           p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters);
+                           p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters,
+                           residual);
     return hip_status(hipGetLastError(), "mfma gemm launch");
 }
 
 /* M <= 16 rows of x against a tile-order weight. */
 template <int OUT>
 int launch_mfma(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
-                int K, hipStream_t stream) {
+                int K, hipStream_t stream, uint16_t *residual = nullptr) {
     const MfmaPlan p = plan_mfma(M, N, K);
     float *partial = nullptr;
     unsigned *counters = nullptr;
@@ -1532,10 +1545,10 @@ int launch_mfma(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, v
         if (st) return st;
     }
     switch (p.xpre) {
-        case 1: return launch_mfma_x<OUT, 1>(p, x, M, w, s, out, N, K, partial, counters, stream);
-        case 2: return launch_mfma_x<OUT, 2>(p, x, M, w, s, out, N, K, partial, counters, stream);
-        case 4: return launch_mfma_x<OUT, 4>(p, x, M, w, s, out, N, K, partial, counters, stream);
-        default: return launch_mfma_x<OUT, 8>(p, x, M, w, s, out, N, K, partial, counters, stream);
+        case 1: return launch_mfma_x<OUT, 1>(p, x, M, w, s, out, N, K, partial, counters, stream, residual);
+        case 2: return launch_mfma_x<OUT, 2>(p, x, M, w, s, out, N, K, partial, counters, stream, residual);
+        case 4: return launch_mfma_x<OUT, 4>(p, x, M, w, s, out, N, K, partial, counters, stream, residual);
+        default: return launch_mfma_x<OUT, 8>(p, x, M, w, s, out, N, K, partial, counters, stream, residual);
     }
 }
 
@@ -1791,6 +1804,11 @@ extern "C" int mlp_int4_residual_norm_bf16(uint16_t *residual, const uint16_t *s
         /* the down kernel adds the output into the (already updated) residual itself */
         st = launch_xwave<false>(act, dnp, dns, out, hidden, inter, s, residual, nullptr);
         if (st <= 0) return st;
+    }
+    if (M >= 2 && M <= 16) { /* the few-row or MFMA down kernel adds into the residual */
+        st = launch_rows<false, false>(act, M, dnp, dns, out, hidden, inter, s, nullptr, residual);
+        if (st > 0) st = launch_mfma<kOutBf16>(act, M, dnp, dns, out, hidden, inter, s, residual);
+        return st;
     }
     st = run_rows<kOutBf16>(act, M, dnp, dns, out, hidden, inter, s);
     if (st) return st;
