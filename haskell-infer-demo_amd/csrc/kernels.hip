@@ -797,31 +797,30 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
     /* 3b. NORM: each staged row becomes its RMSNorm, BF16(x * rsqrt(sum x^2 / K + eps) *
      * (norm_bias + w)) in the FP32 order of the reference's norm (FlashInfer RMSNorm /
      * GemmaRMSNorm behind csrc/kernels/flashinfer_norm.cu:22-76). Wave m sums row m's squares
-     * (a fixed order: per lane, then DPP within rows of 16 and shuffles across them; W >= M for
-     * every launch with NORM), then every thread normalises its staged chunks in place. The
-     * weight loads issued above keep streaming meanwhile. */
+     * (W >= M for every launch with NORM), then every thread normalises its staged chunks in
+     * place. The weight loads issued above keep streaming meanwhile. */
     if (NORM) {
         if (wave < M) {
-            float ss = 0.0f;
+            /* the sum of squares in FP64 (each square of a BF16 value is exact there, and the
+             * sum of up to 2^20 of them rounds far below FP32's step), the scale formed in FP64
+             * and rounded once to FP32: the correctly rounded scale whatever the summation
+             * order, so this prologue and the FP64 restatement of the norm agree exactly */
+            double ss = 0.0;
             for (int j = lane; j < P * 32; j += 64) { /* row m's chunks: (pair, chunk, a) */
                 const int pp = j >> 5, c = (j >> 1) & 15, aa = j & 1;
                 const uint4 ch = smem4[(pp * 16 + c) * 2 * M + 2 * wave + aa];
                 const uint32_t w4[4] = {ch.x, ch.y, ch.z, ch.w};
 #pragma unroll
                 for (int q2 = 0; q2 < 4; ++q2) {
-                    const float lo = bf16_widen((uint16_t)(w4[q2] & 0xFFFFu));
-                    const float hi = bf16_widen((uint16_t)(w4[q2] >> 16));
-                    ss = fmaf(lo, lo, ss);
-                    ss = fmaf(hi, hi, ss);
+                    const double lo = bf16_widen((uint16_t)(w4[q2] & 0xFFFFu));
+                    const double hi = bf16_widen((uint16_t)(w4[q2] >> 16));
+                    ss = fma(lo, lo, ss);
+                    ss = fma(hi, hi, ss);
                 }
             }
-            ss += dpp_f32<kDppQuadSwap1>(ss);
-            ss += dpp_f32<kDppQuadSwap2>(ss);
-            ss += dpp_f32<kDppRowRor4>(ss);
-            ss += dpp_f32<kDppRowRor8>(ss);
-            ss += __shfl_xor(ss, 16);
-            ss += __shfl_xor(ss, 32);
-            if (lane == 0) rms[wave] = 1.0f / sqrtf(ss / (float)K + eps);
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
+            if (lane == 0) rms[wave] = (float)(1.0 / sqrt(ss / (double)K + (double)eps));
         }
         __syncthreads();
         for (int pos = tid; pos < nlds; pos += W * 64) {
