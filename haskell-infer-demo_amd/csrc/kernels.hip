@@ -240,25 +240,29 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
                 xv[it] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
             }
         }
-        float ss = 0.0f;
+        /* the sum of squares in FP64 and the scale rounded once to FP32: the correctly
+         * rounded scale whatever the summation order (each square of a BF16 value is exact in
+         * FP64); one double a wave in the reduction area */
+        double ss = 0.0;
 #pragma unroll
         for (int it = 0; it < kXIters; ++it) {
             const uint32_t w4[4] = {xv[it].x, xv[it].y, xv[it].z, xv[it].w};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const float lo = bf16_widen((uint16_t)(w4[q] & 0xFFFFu));
-                const float hi = bf16_widen((uint16_t)(w4[q] >> 16));
-                ss = fmaf(lo, lo, ss);
-                ss = fmaf(hi, hi, ss);
+                const double lo = bf16_widen((uint16_t)(w4[q] & 0xFFFFu));
+                const double hi = bf16_widen((uint16_t)(w4[q] >> 16));
+                ss = fma(lo, lo, ss);
+                ss = fma(hi, hi, ss);
             }
         }
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
-        if (lane == 0) red[wave] = ss;
+        double *dred = reinterpret_cast<double *>(red);
+        if (lane == 0) dred[wave] = ss;
         __syncthreads();
-        float total = 0.0f;
-        for (int w = 0; w < W; ++w) total += red[w];
-        const float rms = 1.0f / sqrtf(total / (float)K + eps);
+        double total = 0.0;
+        for (int w = 0; w < W; ++w) total += dred[w];
+        const float rms = (float)(1.0 / sqrt(total / (double)K + (double)eps));
 #pragma unroll
         for (int it = 0; it < kXIters; ++it) {
             uint32_t w4[4] = {xv[it].x, xv[it].y, xv[it].z, xv[it].w};
@@ -1035,7 +1039,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t *__restrict__ out
                                                       const uint16_t *__restrict__ w, int cols,
                                                       float bias, float eps,
                                                       const uint16_t *sub) {
-    __shared__ float red[4];
+    __shared__ double red[4];
     const int chunks = cols >> 3;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + (size_t)blockIdx.x * cols, (uint32_t)cols * 2);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(w, (uint32_t)cols * 2);
@@ -1061,24 +1065,26 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t *__restrict__ out
             if (i < chunks) xrow[i] = xv[c];
         }
     }
-    float ss = 0.0f;
+    /* the sum of squares in FP64 and the scale rounded once to FP32: the correctly rounded
+     * scale whatever the summation order (each square of a BF16 value is exact in FP64) */
+    double ss = 0.0;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const uint32_t w4[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float lo = bf16_widen((uint16_t)(w4[q] & 0xFFFFu));
-            const float hi = bf16_widen((uint16_t)(w4[q] >> 16));
-            ss = fmaf(lo, lo, ss);
-            ss = fmaf(hi, hi, ss);
+            const double lo = bf16_widen((uint16_t)(w4[q] & 0xFFFFu));
+            const double hi = bf16_widen((uint16_t)(w4[q] >> 16));
+            ss = fma(lo, lo, ss);
+            ss = fma(hi, hi, ss);
         }
     }
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
-    const float total = red[0] + red[1] + red[2] + red[3];
-    const float rms = 1.0f / sqrtf(total / (float)cols + eps);
+    const double total = (red[0] + red[1]) + (red[2] + red[3]);
+    const float rms = (float)(1.0 / sqrt(total / (double)cols + (double)eps));
     uint4 *orow = reinterpret_cast<uint4 *>(out + (size_t)blockIdx.x * cols);
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
