@@ -157,6 +157,30 @@ def test_few_rows_parity(cuda, m):
     assert_parity(act, oracle.silu_mul_packed(mid, m, inter), f"gate/up M={m}")
 
 
+def test_random_shapes_parity(cuda):
+    """Seeded random shapes across the routing boundaries (group-pair counts from 1 to 40, the
+    staged-row LDS limits, M from 1 to 20 including the 16-row slicing), through gemm_int4_bf16
+    and the fused gate/up, each against the oracle."""
+    rng = np.random.default_rng(2026)
+    for case in range(40):
+        m = int(rng.integers(1, 21))
+        k = 128 * int(rng.integers(1, 81))
+        n = 8 * int(rng.integers(1, 65))
+        say(f"random case {case}: M={m} N={n} K={k}")
+        p, s = make_weight(n, k, seed=1000 + case)
+        x = oracle.synth_activation(m, k, seed=2000 + case)
+        w = w4a16.TiledWeight.from_artifact(p, s, n, k, device=cuda)
+        out = from_dev(w4a16.gemm_int4_bf16(to_dev(x, cuda), w))
+        assert_parity(out, oracle.gemm_bf16(x, p, s, n, k), f"random gemm M={m} N={n} K={k}")
+        if n % 8 == 0 and (n // 2) % 4 == 0:
+            inter = n // 2
+            gu = w4a16.TiledWeight.from_artifact(p, s, n, k, pair=True, device=cuda)
+            act = from_dev(w4a16.gate_up_silu(to_dev(x, cuda), gu))
+            mid = oracle.gemm_bf16(x, p, s, n, k)
+            assert_parity(act, oracle.silu_mul_packed(mid, m, inter),
+                          f"random gate/up M={m} I={inter} K={k}")
+
+
 def test_long_k_routes(cuda):
     """K past the block-staged kernel: a pair operand at M = 1 (hidden 32768) runs the MFMA form
     with one live row; M = 4 at K = 65536 (the MFMA form, 64 K splits)."""
