@@ -1445,9 +1445,11 @@ int device_cus() {
 }
 
 /* Split-K scratch for the MFMA form: FP32 partials and per-tile-pair arrival counters, one set
- * per device, grown on demand (growth synchronises the device; counters are zeroed when
- * allocated and every kernel leaves them zero). Calls that overlap in time on one device share
- * it, so they must be ordered on one stream. */
+ * per device, grown on demand (growth allocates, so it cannot happen under graph capture, and
+ * synchronises the device; counters are zeroed when allocated and every kernel leaves them
+ * zero). Outgrown buffers stay allocated until the process ends (at most the size of the current
+ * one in total, since sizes double), so graphs captured before a growth stay valid. Calls that
+ * overlap in time on one device share the scratch, so they must be ordered on one stream. */
 struct SplitScratch {
     float *partial = nullptr;
     size_t partial_bytes = 0;
@@ -1467,7 +1469,8 @@ int split_scratch(size_t partial_bytes, size_t ncounters, float **partial, unsig
     if (sc.partial_bytes < partial_bytes) {
         size_t want = (size_t)4 << 20;
         while (want < partial_bytes) want *= 2;
-        if (sc.partial) (void)hipFree(sc.partial);
+        /* the outgrown buffer is kept, not freed: a kernel still in flight, or a graph
+         * captured earlier, may hold its address */
         sc.partial = nullptr;
         sc.partial_bytes = 0;
         if (hipMalloc((void **)&sc.partial, want) != hipSuccess)
@@ -1477,8 +1480,7 @@ int split_scratch(size_t partial_bytes, size_t ncounters, float **partial, unsig
     if (sc.ncounters < ncounters) {
         size_t want = 65536;
         while (want < ncounters) want *= 2;
-        if (sc.counters) (void)hipFree(sc.counters);
-        sc.counters = nullptr;
+        sc.counters = nullptr; /* kept, as above; every kernel leaves its counters zero */
         sc.ncounters = 0;
         if (hipMalloc((void **)&sc.counters, want * sizeof(unsigned)) != hipSuccess)
             return set_error(W4A16_ERR_ALLOC, "split-K counters: hipMalloc failed");
