@@ -32,6 +32,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <mutex>
 
 #include "common.h"
@@ -1261,13 +1262,18 @@ int launch_xwave_np(const uint16_t *x, const uint8_t *w, const uint16_t *s, void
 }
 
 /* The wave-local kernel for a K of more than kMaxLoads group pairs: up to 48 pairs one block of
- * 16 waves a tile; beyond, the tile split over BS blocks of 8 waves holding at most 3 pairs each
+ * 16 waves a tile (12 waves at 33 to 36 pairs); beyond, the tile split over BS blocks of 8 waves holding at most 3 pairs each
  * (K = 17408: 12.9 against 13.7 us). residual / sub: the plan-F2 epilogue (BF16 output only).
  * Returns 1 when K is beyond its shapes. */
 template <bool OUT_F32>
 int launch_xwave(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N, int K,
                  hipStream_t stream, uint16_t *residual = nullptr, const uint16_t *sub = nullptr) {
     const int pairs = (K / 128 + 1) / 2;
+    /* 33 to 36 pairs (K = 8320..9216; C4's down, K = 8704): twelve waves of three pairs,
+     * 7.6-7.7 us against 8.1-8.4 for sixteen waves (interleaved bench runs, one box). At 38
+     * pairs (C1's down) thirteen waves only tie sixteen. */
+    if (pairs > 32 && pairs <= 36)
+        return launch_xwave_np<OUT_F32, 3, 12, 1>(x, w, s, out, N, K, stream, residual, sub);
     switch ((pairs + kXwaveWaves - 1) / kXwaveWaves) {
         case 1: return launch_xwave_np<OUT_F32, 1, kXwaveWaves, 1>(x, w, s, out, N, K, stream, residual, sub);
         case 2: return launch_xwave_np<OUT_F32, 2, kXwaveWaves, 1>(x, w, s, out, N, K, stream, residual, sub);

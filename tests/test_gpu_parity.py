@@ -109,7 +109,9 @@ def test_quantize_device_bit_exact(cuda):
                                  (2304, 4096), (3072, 4096),
                                  # 7 to 12 group pairs: four waves of three pairs a tile,
                                  # including odd group counts
-                                 (64, 1792), (64, 2816), (40, 3072), (16, 2944), (56, 1920)])
+                                 (64, 1792), (64, 2816), (40, 3072), (16, 2944), (56, 1920),
+                                 # 33 to 36 pairs: twelve waves of three pairs a tile
+                                 (512, 8448 + 128), (128, 8704), (64, 9216)])
 def test_gemv_parity(cuda, n, k):
     say(f"gemv n={n} k={k}")
     p, s = make_weight(n, k, seed=n + k)
