@@ -1231,6 +1231,9 @@ template <bool PAIR, bool OUT_F32, int TB, int SK, int NL>
 int launch_gemv_cfg(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N,
                     int K, hipStream_t stream, const NormArgs *norm = nullptr) {
     const int tiles = N / 8;
+    if (SK * NL < (K / 128 + 1) / 2)
+        return set_error(W4A16_ERR_CONFIG, "internal: a %d x %d gemv shape covers %d of %d group pairs",
+                         SK, NL, SK * NL, (K / 128 + 1) / 2);
     if (norm)
         hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK, true, NL>),
                            dim3((tiles + TB - 1) / TB), dim3(TB * SK * 64), gemv_smem(K, TB * SK),
@@ -1248,6 +1251,9 @@ template <bool OUT_F32, int NP, int SK, int BS, bool PAIR = false>
 int launch_xwave_np(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N,
                     int K, hipStream_t stream, uint16_t *residual = nullptr,
                     const uint16_t *sub = nullptr) {
+    if (SK * BS * NP < (K / 128 + 1) / 2)
+        return set_error(W4A16_ERR_CONFIG, "internal: a %d x %d x %d wave-local shape covers %d of %d "
+                         "group pairs", BS, SK, NP, BS * SK * NP, (K / 128 + 1) / 2);
     float *partial = nullptr;
     unsigned *counters = nullptr;
     if (BS > 1) {
@@ -1342,6 +1348,9 @@ template <bool PAIR, bool OUT_F32, int TB, int SK, int NL>
 int launch_rows_mi(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
                    int N, int K, hipStream_t stream, const NormArgs *norm = nullptr,
                    uint16_t *residual = nullptr) {
+    if (SK * NL < (K / 128 + 1) / 2)
+        return set_error(W4A16_ERR_CONFIG, "internal: a %d x %d few-row shape covers %d of %d group pairs",
+                         SK, NL, SK * NL, (K / 128 + 1) / 2);
     const size_t smem = rows_smem(M, K, TB * SK, norm != nullptr);
     if (smem > kMaxLds) return 1;
     if (norm && TB * SK < M) return 1; /* the prologue gives each row a wave */
