@@ -19,6 +19,10 @@
  *   - `stream` is a hipStream_t (NULL = the default stream). Device entry points are
  *     asynchronous on it and perform no host synchronisation.
  *   - Device pointers must come from hipMalloc (or a torch CUDA tensor) on the current device.
+ *   - Compute calls that overlap in time on one device must be ordered on one stream: the
+ *     split-K kernels of the small-M path share one per-device scratch buffer. The first call
+ *     of a shape may grow that buffer (an allocation and a device synchronisation), so make it
+ *     before capturing calls into a HIP graph.
  */
 #ifndef W4A16_H
 #define W4A16_H
@@ -135,7 +139,8 @@ int mlp_int4_partial_f32(const uint16_t *normed, const uint8_t *gu_packed,
                          int hidden, int intermediate, void *stream);
 
 /* RMSNorm of `rows` rows of `cols` BF16 values: out = BF16(x * rsqrt(mean(x^2) + eps) * (b + w)),
- * b = 1 for norm_style 0 (Gemma, weight + 1) and 0 for norm_style 1 (plain), FP32 arithmetic.
+ * b = 1 for norm_style 0 (Gemma, weight + 1) and 0 for norm_style 1 (plain); the sum of
+ * squares in FP64, the scale rounded once to FP32, the products in FP32.
  * Replaces kernel_gemma_rms_norm / kernel_rms_norm_plain (reference
  * csrc/kernels/flashinfer_norm.cu:22-76, chosen by layer_norm, csrc/kernels/layers.cu:16-25),
  * with their refusals (rows < 0, cols <= 0, eps not finite and positive; rows == 0 no-op), plus
