@@ -142,6 +142,42 @@ def _ptr(t):
     return t.data_ptr()
 
 
+def _dev(t, nbytes, elem, what, device=None):
+    """Check a device operand before its address reaches a kernel: a contiguous CUDA tensor with
+    `elem`-byte elements (BF16 bits as int16/bfloat16, FP32, u8) holding at least `nbytes`, on
+    `device` when given. The kernels trust their extents, so a short or strided buffer would be
+    read or written out of bounds on the GPU; this raises W4A16Error instead."""
+    if not hasattr(t, "data_ptr") or not hasattr(t, "is_cuda"):
+        raise W4A16Error(W4A16_ERR_CONFIG, f"{what}: expected a CUDA tensor, got {type(t).__name__}")
+    if not t.is_cuda:
+        raise W4A16Error(W4A16_ERR_CONFIG, f"{what}: tensor is on {t.device}, not a GPU")
+    if device is not None and t.device != device:
+        raise W4A16Error(W4A16_ERR_CONFIG, f"{what}: tensor is on {t.device}, the call on {device}")
+    if not t.is_contiguous():
+        raise W4A16Error(W4A16_ERR_CONFIG, f"{what}: tensor is not contiguous")
+    if t.element_size() != elem:
+        raise W4A16Error(W4A16_ERR_CONFIG,
+                         f"{what}: {t.dtype} has {t.element_size()}-byte elements, expected {elem}")
+    have = t.numel() * elem
+    if have < nbytes:
+        raise W4A16Error(W4A16_ERR_CONFIG, f"{what}: {have} bytes, the call needs {nbytes}")
+    return t.data_ptr()
+
+
+def _check_ffn(h, inter, gu, dn, what):
+    """The gate/up pair is [2I, H] and the down weight [H, I]."""
+    if not (gu.pair and gu.k == h and gu.n == 2 * inter and dn.n == h and dn.k == inter):
+        raise W4A16Error(W4A16_ERR_CONFIG,
+                         f"{what}: operands [{gu.n}, {gu.k}] (pair={gu.pair}) and [{dn.n}, {dn.k}] "
+                         f"do not form an FFN of hidden {h}")
+
+
+def _weight(w, what, device):
+    """Device operands of a TiledWeight, checked against its extents."""
+    return (_dev(w.packed, w.n * w.k // 2, 1, f"{what} packed", device),
+            _dev(w.scales, w.n * (w.k // GROUP) * 2, 2, f"{what} scales", device))
+
+
 def _stream(stream):
     if stream is None:
         import torch
@@ -231,10 +267,13 @@ class TiledWeight:
     def from_device_artifact(cls, p, s, n, k, pair=False, stream=None):
         import torch
 
-        pt = torch.empty_like(p)
-        st = torch.empty_like(s)
-        _check(lib.w4a16_tile_pack_device(n, k, int(pair), p.data_ptr(), s.data_ptr(),
-                                          pt.data_ptr(), st.data_ptr(), _stream(stream)),
+        layout_init(n, k)
+        pp = _dev(p, n * k // 2, 1, "tile_pack_device packed")
+        sp = _dev(s, n * (k // GROUP) * 2, 2, "tile_pack_device scales", p.device)
+        pt = torch.empty(n * k // 2, dtype=torch.uint8, device=p.device)
+        st = torch.empty(n * (k // GROUP), dtype=s.dtype, device=p.device)
+        _check(lib.w4a16_tile_pack_device(n, k, int(pair), pp, sp, pt.data_ptr(), st.data_ptr(),
+                                          _stream(stream)),
                "tile_pack_device")
         return cls(pt, st, n, k, pair)
 
@@ -242,8 +281,8 @@ class TiledWeight:
         import torch
 
         out = torch.empty((self.n, self.k), dtype=torch.float32, device=self.packed.device)
-        _check(lib.w4a16_dequant_tiled_device(self.n, self.k, int(self.pair),
-                                              self.packed.data_ptr(), self.scales.data_ptr(),
+        wp, ws = _weight(self, "dequant_tiled_device", self.packed.device)
+        _check(lib.w4a16_dequant_tiled_device(self.n, self.k, int(self.pair), wp, ws,
                                               out.data_ptr(), _stream(stream)),
                "dequant_tiled_device")
         return out
@@ -255,10 +294,12 @@ def quantize_device(weights, stream=None):
 
     n, k = weights.shape
     layout_init(n, k)
+    weights = weights.contiguous()
+    _dev(weights, n * k * 4, 4, "quantize_device weights")
     packed = torch.empty(n * k // 2, dtype=torch.uint8, device=weights.device)
     scales = torch.empty(n * (k // GROUP), dtype=torch.int16, device=weights.device)
     status = torch.zeros(1, dtype=torch.int32, device=weights.device)
-    _check(lib.w4a16_quantize_device(n, k, weights.contiguous().data_ptr(), packed.data_ptr(),
+    _check(lib.w4a16_quantize_device(n, k, weights.data_ptr(), packed.data_ptr(),
                                      scales.data_ptr(), status.data_ptr(), _stream(stream)),
            "quantize_device")
     if int(status.item()) != 0:
@@ -277,17 +318,25 @@ def gemm_int4_bf16(a, w, out=None, stream=None):
     import torch
 
     m = a.shape[0]
+    if a.dim() != 2 or a.shape[1] != w.k:
+        raise W4A16Error(W4A16_ERR_CONFIG, f"gemm_int4_bf16: a is {tuple(a.shape)}, the weight "
+                                           f"takes K={w.k}")
     if out is None:
         out = torch.empty((m, w.n), dtype=a.dtype, device=a.device)
-    _check(lib.gemm_int4_bf16(a.data_ptr(), w.packed.data_ptr(), w.scales.data_ptr(),
-                              out.data_ptr(), m, w.n, w.k, GROUP, _stream(stream)),
+    ap = _dev(a, m * w.k * 2, 2, "gemm_int4_bf16 a")
+    wp, ws = _weight(w, "gemm_int4_bf16", a.device)
+    op = _dev(out, m * w.n * 2, 2, "gemm_int4_bf16 out", a.device)
+    _check(lib.gemm_int4_bf16(ap, wp, ws, op, m, w.n, w.k, GROUP, _stream(stream)),
            "gemm_int4_bf16")
     return out
 
 
 def kernel_silu_mul_packed(out, packed, tokens, intermediate, stream=None):
-    _check(lib.silu_mul_packed_bf16(out.data_ptr(), packed.data_ptr(), tokens, intermediate,
-                                    _stream(stream)), "silu_mul_packed")
+    need = max(tokens, 0) * max(intermediate, 0) * 2
+    op = _dev(out, need, 2, "silu_mul_packed out")
+    pp = _dev(packed, 2 * need, 2, "silu_mul_packed packed", out.device)
+    _check(lib.silu_mul_packed_bf16(op, pp, tokens, intermediate, _stream(stream)),
+           "silu_mul_packed")
     return out
 
 
@@ -296,10 +345,14 @@ def gate_up_silu(x, gu, act=None, stream=None):
 
     m, h = x.shape
     inter = gu.n // 2
+    if h != gu.k:
+        raise W4A16Error(W4A16_ERR_CONFIG, f"gate_up_silu: x has {h} columns, the pair takes {gu.k}")
     if act is None:
         act = torch.empty((m, inter), dtype=x.dtype, device=x.device)
-    _check(lib.gate_up_silu_int4_bf16(x.data_ptr(), gu.packed.data_ptr(), gu.scales.data_ptr(),
-                                      act.data_ptr(), m, h, inter, _stream(stream)),
+    xp = _dev(x, m * h * 2, 2, "gate_up_silu x")
+    wp, ws = _weight(gu, "gate_up_silu", x.device)
+    ap = _dev(act, m * inter * 2, 2, "gate_up_silu act", x.device)
+    _check(lib.gate_up_silu_int4_bf16(xp, wp, ws, ap, m, h, inter, _stream(stream)),
            "gate_up_silu")
     return act
 
@@ -310,15 +363,20 @@ def mlp_int4(x, gu, dn, out=None, act_ws=None, partial_f32=False, stream=None):
 
     m, h = x.shape
     inter = gu.n // 2
+    _check_ffn(h, inter, gu, dn, "mlp_int4")
     if act_ws is None:
         act_ws = torch.empty((m, inter), dtype=x.dtype, device=x.device)
     if out is None:
         out = torch.empty((m, h), dtype=torch.float32 if partial_f32 else x.dtype,
                           device=x.device)
+    osz = 4 if partial_f32 else 2
+    xp = _dev(x, m * h * 2, 2, "mlp_int4 x")
+    gp, gs = _weight(gu, "mlp_int4 gate/up", x.device)
+    dp, ds = _weight(dn, "mlp_int4 down", x.device)
+    op = _dev(out, m * h * osz, osz, "mlp_int4 out", x.device)
+    wsp = _dev(act_ws, m * inter * 2, 2, "mlp_int4 act_ws", x.device)
     fn = lib.mlp_int4_partial_f32 if partial_f32 else lib.mlp_int4_bf16
-    _check(fn(x.data_ptr(), gu.packed.data_ptr(), gu.scales.data_ptr(), dn.packed.data_ptr(),
-              dn.scales.data_ptr(), out.data_ptr(), act_ws.data_ptr(), m, h, inter,
-              _stream(stream)), "mlp_int4")
+    _check(fn(xp, gp, gs, dp, ds, op, wsp, m, h, inter, _stream(stream)), "mlp_int4")
     return out
 
 
@@ -329,8 +387,11 @@ def rmsnorm(x, weight, norm_style, eps, out=None, stream=None):
     rows, cols = x.shape
     if out is None:
         out = torch.empty_like(x)
-    _check(lib.w4a16_rmsnorm_bf16(out.data_ptr(), x.data_ptr(), weight.data_ptr(), cols, rows,
-                                  norm_style, eps, _stream(stream)), "w4a16_rmsnorm_bf16")
+    xp = _dev(x, rows * cols * 2, 2, "rmsnorm x")
+    wp = _dev(weight, cols * 2, 2, "rmsnorm weight", x.device)
+    op = _dev(out, rows * cols * 2, 2, "rmsnorm out", x.device)
+    _check(lib.w4a16_rmsnorm_bf16(op, xp, wp, cols, rows, norm_style, eps, _stream(stream)),
+           "w4a16_rmsnorm_bf16")
     return out
 
 
@@ -341,15 +402,23 @@ def mlp_int4_norm(residual, norm_w, norm_style, eps, gu, dn, out=None, ws=None, 
 
     m, h = residual.shape
     inter = gu.n // 2
+    _check_ffn(h, inter, gu, dn, "mlp_int4_norm")
     if ws is None:
         ws = torch.empty((m, h + inter), dtype=residual.dtype, device=residual.device)
     if out is None:
         out = torch.empty((m, h), dtype=torch.float32 if partial_f32 else residual.dtype,
                           device=residual.device)
+    dev = residual.device
+    osz = 4 if partial_f32 else 2
+    rp = _dev(residual, m * h * 2, 2, "mlp_int4_norm residual")
+    nwp = _dev(norm_w, h * 2, 2, "mlp_int4_norm norm_w", dev)
+    gp, gs = _weight(gu, "mlp_int4_norm gate/up", dev)
+    dp, ds = _weight(dn, "mlp_int4_norm down", dev)
+    op = _dev(out, m * h * osz, osz, "mlp_int4_norm out", dev)
+    wsp = _dev(ws, m * (h + inter) * 2, 2, "mlp_int4_norm ws", dev)
     fn = lib.mlp_int4_norm_partial_f32 if partial_f32 else lib.mlp_int4_norm_bf16
-    _check(fn(residual.data_ptr(), norm_w.data_ptr(), norm_style, eps, gu.packed.data_ptr(),
-              gu.scales.data_ptr(), dn.packed.data_ptr(), dn.scales.data_ptr(), out.data_ptr(),
-              ws.data_ptr(), m, h, inter, _stream(stream)), "mlp_int4_norm")
+    _check(fn(rp, nwp, norm_style, eps, gp, gs, dp, ds, op, wsp, m, h, inter, _stream(stream)),
+           "mlp_int4_norm")
     return out
 
 
@@ -361,15 +430,22 @@ def mlp_int4_residual_norm(residual, sublayer, norm_w, norm_style, eps, gu, dn, 
 
     m, h = residual.shape
     inter = gu.n // 2
+    _check_ffn(h, inter, gu, dn, "mlp_int4_residual_norm")
     if ws is None:
         ws = torch.empty((m, h + inter), dtype=residual.dtype, device=residual.device)
     if out is None:
         out = torch.empty((m, h), dtype=residual.dtype, device=residual.device)
-    _check(lib.mlp_int4_residual_norm_bf16(residual.data_ptr(), sublayer.data_ptr(),
-                                           norm_w.data_ptr(), norm_style, eps, gu.packed.data_ptr(),
-                                           gu.scales.data_ptr(), dn.packed.data_ptr(),
-                                           dn.scales.data_ptr(), out.data_ptr(), ws.data_ptr(), m, h,
-                                           inter, _stream(stream)), "mlp_int4_residual_norm")
+    dev = residual.device
+    rp = _dev(residual, m * h * 2, 2, "mlp_int4_residual_norm residual")
+    sp = _dev(sublayer, m * h * 2, 2, "mlp_int4_residual_norm sublayer", dev)
+    nwp = _dev(norm_w, h * 2, 2, "mlp_int4_residual_norm norm_w", dev)
+    gp, gs = _weight(gu, "mlp_int4_residual_norm gate/up", dev)
+    dp, ds = _weight(dn, "mlp_int4_residual_norm down", dev)
+    op = _dev(out, m * h * 2, 2, "mlp_int4_residual_norm out", dev)
+    wsp = _dev(ws, m * (h + inter) * 2, 2, "mlp_int4_residual_norm ws", dev)
+    _check(lib.mlp_int4_residual_norm_bf16(rp, sp, nwp, norm_style, eps, gp, gs, dp, ds, op, wsp,
+                                           m, h, inter, _stream(stream)),
+           "mlp_int4_residual_norm")
     return out
 
 
@@ -460,9 +536,11 @@ class Engine:
         if out is None:
             out = torch.empty((m, self.hidden), dtype=torch.float32 if partial_f32 else normed.dtype,
                               device=normed.device)
+        osz = 4 if partial_f32 else 2
+        np_ = _dev(normed, m * self.hidden * 2, 2, "engine_ffn_forward normed")
+        op = _dev(out, m * self.hidden * osz, osz, "engine_ffn_forward out", normed.device)
         fn = lib.engine_ffn_forward_partial_f32 if partial_f32 else lib.engine_ffn_forward
-        _check(fn(self.handle, layer, normed.data_ptr(), out.data_ptr(), m, _stream(stream)),
-               "engine_ffn_forward")
+        _check(fn(self.handle, layer, np_, op, m, _stream(stream)), "engine_ffn_forward")
         return out
 
     def forward_norm(self, layer, residual, norm_w, norm_style, eps, out=None, partial_f32=False,
@@ -475,10 +553,15 @@ class Engine:
             out = torch.empty((m, self.hidden),
                               dtype=torch.float32 if partial_f32 else residual.dtype,
                               device=residual.device)
+        osz = 4 if partial_f32 else 2
+        dev = residual.device
+        rp = _dev(residual, m * self.hidden * 2, 2, "engine_ffn_forward_norm residual")
+        nwp = _dev(norm_w, self.hidden * 2, 2, "engine_ffn_forward_norm norm_w", dev)
+        op = _dev(out, m * self.hidden * osz, osz, "engine_ffn_forward_norm out", dev)
         fn = (lib.engine_ffn_forward_norm_partial_f32 if partial_f32
               else lib.engine_ffn_forward_norm)
-        _check(fn(self.handle, layer, residual.data_ptr(), norm_w.data_ptr(), norm_style, eps,
-                  out.data_ptr(), m, _stream(stream)), "engine_ffn_forward_norm")
+        _check(fn(self.handle, layer, rp, nwp, norm_style, eps, op, m, _stream(stream)),
+               "engine_ffn_forward_norm")
         return out
 
     def forward_residual_norm(self, layer, residual, sublayer, norm_w, norm_style, eps, out=None,
@@ -489,9 +572,12 @@ class Engine:
         m = residual.shape[0]
         if out is None:
             out = torch.empty((m, self.hidden), dtype=residual.dtype, device=residual.device)
-        _check(lib.engine_ffn_forward_residual_norm(self.handle, layer, residual.data_ptr(),
-                                                    sublayer.data_ptr(), norm_w.data_ptr(),
-                                                    norm_style, eps, out.data_ptr(), m,
-                                                    _stream(stream)),
+        dev = residual.device
+        rp = _dev(residual, m * self.hidden * 2, 2, "engine_ffn_forward_residual_norm residual")
+        sp = _dev(sublayer, m * self.hidden * 2, 2, "engine_ffn_forward_residual_norm sublayer", dev)
+        nwp = _dev(norm_w, self.hidden * 2, 2, "engine_ffn_forward_residual_norm norm_w", dev)
+        op = _dev(out, m * self.hidden * 2, 2, "engine_ffn_forward_residual_norm out", dev)
+        _check(lib.engine_ffn_forward_residual_norm(self.handle, layer, rp, sp, nwp, norm_style,
+                                                    eps, op, m, _stream(stream)),
                "engine_ffn_forward_residual_norm")
         return out

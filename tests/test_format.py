@@ -175,3 +175,25 @@ def test_gemm_shape_limits_without_touching_the_device():
         w4a16.W4A16_ERR_CONFIG
     assert lib.gemm_int4_bf16(d, d, d, d, 2, 65536, 131072, 128, None) == w4a16.W4A16_ERR_CONFIG
     assert "4 GiB" in w4a16.last_error()
+
+
+def test_python_wrappers_refuse_bad_buffers_before_any_launch():
+    """The ctypes wrappers check every device operand (CUDA, contiguous, element width, size,
+    device) before its address reaches the library; host tensors and mismatched FFN operands
+    are refused here without a GPU."""
+    import torch
+
+    n, k = 8, 256
+    w = w4a16.TiledWeight(torch.zeros(n * k // 2, dtype=torch.uint8),
+                          torch.zeros(n * k // 128, dtype=torch.int16), n, k, False)
+    a = torch.zeros(1, k, dtype=torch.int16)
+    with pytest.raises(w4a16.W4A16Error, match="not a GPU"):
+        w4a16.gemm_int4_bf16(a, w, out=torch.zeros(1, n, dtype=torch.int16))
+    with pytest.raises(w4a16.W4A16Error, match="takes K=256"):
+        w4a16.gemm_int4_bf16(torch.zeros(1, 128, dtype=torch.int16), w)
+    with pytest.raises(w4a16.W4A16Error, match="expected a CUDA tensor"):
+        w4a16._dev(np.zeros(4, dtype=np.int16), 8, 2, "probe")
+    gu = w4a16.TiledWeight(None, None, 2 * 128, k, True)
+    dn = w4a16.TiledWeight(None, None, k, 256, False)   # down must be [H, I] = [256, 128]
+    with pytest.raises(w4a16.W4A16Error, match="do not form an FFN"):
+        w4a16.mlp_int4(a, gu, dn)

@@ -523,3 +523,28 @@ def test_reference_kernel_gate_shapes():
     out = np.zeros((1, 128), np.uint16)
     assert w4a16.lib.test_gemm_int4(out.ctypes.data, out.ctypes.data, bad.ctypes.data,
                                     np.zeros(128, np.uint16).ctypes.data, 1, 128, 192, 128) != 0
+
+
+def test_wrappers_refuse_short_or_strided_device_buffers(cuda):
+    """A caller-supplied output or workspace that is too small, strided or of the wrong element
+    width is refused before the kernel is launched (the kernels trust their extents)."""
+    import torch
+
+    n, k = 64, 2560
+    p, s = make_weight(n, k, seed=3)
+    w = w4a16.TiledWeight.from_artifact(p, s, n, k, device=cuda)
+    a = to_dev(oracle.synth_activation(2, k, seed=4), cuda)
+    with pytest.raises(w4a16.W4A16Error, match="bytes, the call needs"):
+        w4a16.gemm_int4_bf16(a, w, out=torch.empty((2, n - 8), dtype=torch.int16, device=cuda))
+    with pytest.raises(w4a16.W4A16Error, match="not contiguous"):
+        w4a16.gemm_int4_bf16(a, w, out=torch.empty((n, 2), dtype=torch.int16, device=cuda).t())
+    with pytest.raises(w4a16.W4A16Error, match="4-byte elements"):
+        w4a16.gemm_int4_bf16(a, w, out=torch.empty((2, n), dtype=torch.float32, device=cuda))
+    gup, gus, dp, ds = make_ffn(256, 512)
+    gu = w4a16.TiledWeight.from_artifact(gup, gus, 1024, 256, pair=True, device=cuda)
+    dn = w4a16.TiledWeight.from_artifact(dp, ds, 256, 512, device=cuda)
+    x = to_dev(oracle.synth_activation(4, 256, seed=5), cuda)
+    with pytest.raises(w4a16.W4A16Error, match="act_ws"):
+        w4a16.mlp_int4(x, gu, dn, act_ws=torch.empty((2, 512), dtype=torch.int16, device=cuda))
+    out = from_dev(w4a16.mlp_int4(x, gu, dn))           # the same call with valid buffers
+    assert out.shape == (4, 256)
