@@ -1574,14 +1574,20 @@ int launch_mfma(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, v
     }
 }
 
+/* Every device buffer of the compute entry points starts on a 16-byte boundary: the kernels
+ * move 16 bytes a lane (buffer and direct-to-LDS loads). Allocator pointers always do. */
+bool misaligned(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
+
 /* Shape refusals of the reference wrapper (csrc/kernels/gemm_quant.cu:204-231), plus the
- * tile rules this layout adds (N % 8, group == 128). */
+ * tile rules this layout adds (N % 8, group == 128) and 16-byte aligned buffers. */
 int check_gemm_args(const void *a, const void *p, const void *s, const void *o, int M, int N,
                     int K, int group, const char *what) {
     if (M < 0 || N < 0 || K <= 0 || group <= 0)
         return set_error(W4A16_ERR_CONFIG, "%s: negative extent or nonpositive group", what);
     if (M == 0 || N == 0) return 1; /* no-op */
     if (!a || !p || !s || !o) return set_error(W4A16_ERR_CONFIG, "%s: null buffer", what);
+    if (misaligned(a) || misaligned(p) || misaligned(s) || misaligned(o))
+        return set_error(W4A16_ERR_CONFIG, "%s: device buffers must be 16-byte aligned", what);
     if (K % group != 0)
         return set_error(W4A16_ERR_CONFIG, "%s: K=%d is not a whole number of %d-wide groups",
                          what, K, group);
@@ -1695,6 +1701,8 @@ static int norm_args(const uint16_t *w, int style, float eps, int cols, int rows
         return set_error(W4A16_ERR_CONFIG, "%s: norm_style %d is neither 0 (gemma) nor 1 (plain)",
                          what, style);
     if (rows > 0 && !w) return set_error(W4A16_ERR_CONFIG, "%s: null norm weight", what);
+    if (rows > 0 && misaligned(w))
+        return set_error(W4A16_ERR_CONFIG, "%s: the norm weight must be 16-byte aligned", what);
     na->w = w;
     na->bias = style == 0 ? 1.0f : 0.0f;
     na->eps = eps;
@@ -1721,6 +1729,8 @@ extern "C" int w4a16_rmsnorm_bf16(uint16_t *out, const uint16_t *x, const uint16
     if (st) return st;
     if (rows == 0) return W4A16_OK;
     if (!out || !x) return set_error(W4A16_ERR_CONFIG, "w4a16_rmsnorm_bf16: null buffer");
+    if (misaligned(out) || misaligned(x))
+        return set_error(W4A16_ERR_CONFIG, "w4a16_rmsnorm_bf16: buffers must be 16-byte aligned");
     return launch_rmsnorm(out, x, weight, cols, rows, na.bias, eps, static_cast<hipStream_t>(stream));
 }
 
@@ -1796,6 +1806,8 @@ extern "C" int mlp_int4_residual_norm_bf16(uint16_t *residual, const uint16_t *s
     if (M == 0) return W4A16_OK;
     if (!residual || !sublayer || !ws || !out)
         return set_error(W4A16_ERR_CONFIG, "mlp_int4_residual_norm: null buffer");
+    if (misaligned(sublayer))
+        return set_error(W4A16_ERR_CONFIG, "mlp_int4_residual_norm: the sublayer must be 16-byte aligned");
     if (hidden % 8)
         return set_error(W4A16_ERR_CONFIG, "mlp_int4_residual_norm: hidden=%d is not a multiple of 8",
                          hidden);
@@ -1855,6 +1867,8 @@ extern "C" int silu_mul_packed_bf16(uint16_t *out, const uint16_t *packed, int t
         return set_error(W4A16_ERR_CONFIG, "silu_mul_packed: negative extent");
     if (tokens == 0 || inter == 0) return W4A16_OK;
     if (!out || !packed) return set_error(W4A16_ERR_CONFIG, "silu_mul_packed: null buffer");
+    if (misaligned(out) || misaligned(packed))
+        return set_error(W4A16_ERR_CONFIG, "silu_mul_packed: buffers must be 16-byte aligned");
     const int block = 256;
     hipLaunchKernelGGL(silu_mul_packed_kernel, dim3((inter + block - 1) / block, tokens),
                        dim3(block), 0, static_cast<hipStream_t>(stream), out, packed, tokens,
@@ -1867,6 +1881,8 @@ extern "C" int w4a16_tile_pack_device(long long n, long long k, int pair, const 
                                       uint16_t *scales_tiled, void *stream) {
     if (!packed || !scales || !packed_tiled || !scales_tiled)
         return set_error(W4A16_ERR_CONFIG, "tile_pack_device: null argument");
+    if (misaligned(packed) || misaligned(scales) || misaligned(packed_tiled) || misaligned(scales_tiled))
+        return set_error(W4A16_ERR_CONFIG, "tile_pack_device: device buffers must be 16-byte aligned");
     int st = w4a16_layout_init(n, k, W4A16_GROUP, nullptr, nullptr);
     if (st) return st;
     if (pair != 0 && pair != 1) return set_error(W4A16_ERR_CONFIG, "tile_pack_device: bad pair");
@@ -1883,6 +1899,8 @@ extern "C" int w4a16_dequant_tiled_device(long long n, long long k, int pair,
                                           void *stream) {
     if (!packed_tiled || !scales_tiled || !out)
         return set_error(W4A16_ERR_CONFIG, "dequant_tiled_device: null argument");
+    if (misaligned(packed_tiled) || misaligned(scales_tiled) || misaligned(out))
+        return set_error(W4A16_ERR_CONFIG, "dequant_tiled_device: device buffers must be 16-byte aligned");
     int st = w4a16_layout_init(n, k, W4A16_GROUP, nullptr, nullptr);
     if (st) return st;
     if (pair != 0 && pair != 1) return set_error(W4A16_ERR_CONFIG, "dequant_tiled: bad pair");
@@ -1899,6 +1917,8 @@ extern "C" int w4a16_quantize_device(long long n, long long k, const float *weig
                                      void *stream) {
     if (!weights || !packed || !scales || !status_dev)
         return set_error(W4A16_ERR_CONFIG, "quantize_device: null argument");
+    if (misaligned(weights) || misaligned(packed) || misaligned(scales) || misaligned(status_dev))
+        return set_error(W4A16_ERR_CONFIG, "quantize_device: device buffers must be 16-byte aligned");
     int st = w4a16_layout_init(n, k, W4A16_GROUP, nullptr, nullptr);
     if (st) return st;
     const long long total = n * (k / 128);

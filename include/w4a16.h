@@ -18,7 +18,9 @@
  *     the reason is in the calling thread's w4a16_last_error().
  *   - `stream` is a hipStream_t (NULL = the default stream). Device entry points are
  *     asynchronous on it and perform no host synchronisation.
- *   - Device pointers must come from hipMalloc (or a torch CUDA tensor) on the current device.
+ *   - Device pointers must come from hipMalloc (or a torch CUDA tensor) on the current device
+ *     and start on a 16-byte boundary (the kernels move 16 bytes a lane); a misaligned buffer
+ *     is refused with W4A16_ERR_CONFIG before anything is launched.
  *   - Compute calls that overlap in time on one device must be ordered on one stream: the
  *     split-K kernels of the small-M path share one per-device scratch buffer. The first call
  *     of a shape may grow that buffer (an allocation and a device synchronisation), so make it

@@ -197,3 +197,17 @@ def test_python_wrappers_refuse_bad_buffers_before_any_launch():
     dn = w4a16.TiledWeight(None, None, k, 256, False)   # down must be [H, I] = [256, 128]
     with pytest.raises(w4a16.W4A16Error, match="do not form an FFN"):
         w4a16.mlp_int4(a, gu, dn)
+
+
+def test_device_entries_refuse_misaligned_buffers_without_touching_the_device():
+    """16-byte alignment of every device buffer is checked before any launch (the addresses
+    below are never dereferenced)."""
+    base = 1 << 20
+    st = w4a16.lib.gemm_int4_bf16(base + 2, base, base, base, 1, 64, 256, 128, None)
+    assert st == w4a16.W4A16_ERR_CONFIG and "16-byte aligned" in w4a16.last_error()
+    st = w4a16.lib.w4a16_rmsnorm_bf16(base, base + 8, base, 256, 1, 1, 1e-6, None)
+    assert st == w4a16.W4A16_ERR_CONFIG and "16-byte aligned" in w4a16.last_error()
+    st = w4a16.lib.silu_mul_packed_bf16(base + 4, base, 1, 64, None)
+    assert st == w4a16.W4A16_ERR_CONFIG and "16-byte aligned" in w4a16.last_error()
+    st = w4a16.lib.w4a16_tile_pack_device(8, 256, 0, base, base + 2, base, base, None)
+    assert st == w4a16.W4A16_ERR_CONFIG and "16-byte aligned" in w4a16.last_error()
