@@ -1578,10 +1578,17 @@ int launch_mfma(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, v
  * move 16 bytes a lane (buffer and direct-to-LDS loads). Allocator pointers always do. */
 bool misaligned(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
 
+/* Whether byte ranges [a, a + an) and [b, b + bn) share a byte. A kernel that reads one while
+ * its other blocks write the other would race, so such pairs are refused. */
+bool overlap(const void *a, size_t an, const void *b, size_t bn) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return an && bn && x < y + bn && y < x + an;
+}
+
 /* Shape refusals of the reference wrapper (csrc/kernels/gemm_quant.cu:204-231), plus the
  * tile rules this layout adds (N % 8, group == 128) and 16-byte aligned buffers. */
 int check_gemm_args(const void *a, const void *p, const void *s, const void *o, int M, int N,
-                    int K, int group, const char *what) {
+                    int K, int group, const char *what, size_t out_bytes = 0) {
     if (M < 0 || N < 0 || K <= 0 || group <= 0)
         return set_error(W4A16_ERR_CONFIG, "%s: negative extent or nonpositive group", what);
     if (M == 0 || N == 0) return 1; /* no-op */
@@ -1609,6 +1616,10 @@ int check_gemm_args(const void *a, const void *p, const void *s, const void *o, 
     if ((unsigned long long)N * (unsigned long long)K / 2 >= (1ull << 32))
         return set_error(W4A16_ERR_CONFIG, "%s: a %d x %d operand exceeds the 4 GiB a buffer "
                          "descriptor addresses", what, N, K);
+    const size_t wbytes = (size_t)N * K / 2, sbytes = (size_t)N * (K / 128) * 2;
+    if (overlap(a, (size_t)M * K * 2, o, out_bytes) || overlap(p, wbytes, o, out_bytes) ||
+        overlap(s, sbytes, o, out_bytes))
+        return set_error(W4A16_ERR_CONFIG, "%s: the output overlaps an input", what);
     return 0;
 }
 
@@ -1645,7 +1656,8 @@ static int run_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *
 
 extern "C" int gemm_int4_bf16(const uint16_t *a, const uint8_t *packed, const uint16_t *scales,
                               uint16_t *out, int M, int N, int K, int group, void *stream) {
-    int st = check_gemm_args(a, packed, scales, out, M, N, K, group, "gemm_int4_bf16");
+    int st = check_gemm_args(a, packed, scales, out, M, N, K, group, "gemm_int4_bf16",
+                             (size_t)std::max(M, 0) * std::max(N, 0) * 2);
     if (st) return st > 0 ? W4A16_OK : st;
     return run_rows<kOutBf16>(a, M, packed, scales, out, N, K, static_cast<hipStream_t>(stream));
 }
@@ -1655,7 +1667,7 @@ extern "C" int gate_up_silu_int4_bf16(const uint16_t *x, const uint8_t *gu_packe
                                       int inter, void *stream) {
     if (inter < 0) return set_error(W4A16_ERR_CONFIG, "gate_up_silu: negative intermediate");
     int st = check_gemm_args(x, gu_packed, gu_scales, act, M, 2 * inter, hidden, W4A16_GROUP,
-                             "gate_up_silu_int4_bf16");
+                             "gate_up_silu_int4_bf16", (size_t)std::max(M, 0) * inter * 2);
     if (st) return st > 0 ? W4A16_OK : st;
     return run_rows<kOutPairSilu>(x, M, gu_packed, gu_scales, act, 2 * inter, hidden,
                                   static_cast<hipStream_t>(stream));
@@ -1669,7 +1681,8 @@ static int mlp_common(const uint16_t *normed, const uint8_t *gup, const uint16_t
                          hidden, inter);
     if (M == 0) return W4A16_OK;
     if (!act || !out) return set_error(W4A16_ERR_CONFIG, "mlp_int4: null buffer");
-    int st = check_gemm_args(act, dnp, dns, out, M, hidden, inter, W4A16_GROUP, "mlp_int4 down");
+    int st = check_gemm_args(act, dnp, dns, out, M, hidden, inter, W4A16_GROUP, "mlp_int4 down",
+                             (size_t)M * hidden * (out_f32 ? 4 : 2));
     if (st < 0) return st;
     hipStream_t s = static_cast<hipStream_t>(stream);
     st = gate_up_silu_int4_bf16(normed, gup, gus, act, M, hidden, inter, stream);
@@ -1751,6 +1764,13 @@ static int mlp_norm_common(const uint16_t *residual, const uint16_t *norm_w, int
     if (st < 0) return st;
     st = check_gemm_args(ws, dnp, dns, out, M, hidden, inter, W4A16_GROUP, "mlp_int4_norm down");
     if (st < 0) return st;
+    {
+        const size_t ws_bytes = (size_t)M * (hidden + inter) * 2, row_bytes = (size_t)M * hidden * 2;
+        if (overlap(residual, row_bytes, ws, ws_bytes) ||
+            overlap(out, (size_t)M * hidden * (out_f32 ? 4 : 2), ws, ws_bytes) ||
+            overlap(norm_w, (size_t)hidden * 2, ws, ws_bytes))
+            return set_error(W4A16_ERR_CONFIG, "mlp_int4_norm: the workspace overlaps another buffer");
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint16_t *normed = ws;                          /* [M, hidden] (M > 1) */
     uint16_t *act = ws + (size_t)M * hidden;        /* [M, inter] */
@@ -1817,6 +1837,20 @@ extern "C" int mlp_int4_residual_norm_bf16(uint16_t *residual, const uint16_t *s
     st = check_gemm_args(ws, dnp, dns, out, M, hidden, inter, W4A16_GROUP,
                          "mlp_int4_residual_norm down");
     if (st < 0) return st;
+    {
+        const size_t ws_bytes = (size_t)M * (hidden + inter) * 2, row_bytes = (size_t)M * hidden * 2;
+        if (overlap(residual, row_bytes, ws, ws_bytes) || overlap(sublayer, row_bytes, ws, ws_bytes) ||
+            overlap(out, row_bytes, ws, ws_bytes) || overlap(norm_w, (size_t)hidden * 2, ws, ws_bytes))
+            return set_error(W4A16_ERR_CONFIG,
+                             "mlp_int4_residual_norm: the workspace overlaps another buffer");
+        /* the sublayer may alias the output exactly (the reference's layer_out); the residual,
+         * updated in place beside the output, may not overlap it */
+        if (overlap(residual, row_bytes, out, row_bytes) ||
+            (sublayer != out && overlap(sublayer, row_bytes, out, row_bytes)))
+            return set_error(W4A16_ERR_CONFIG,
+                             "mlp_int4_residual_norm: the output overlaps the residual or, other "
+                             "than exactly, the sublayer");
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint16_t *normed = ws;
     uint16_t *act = ws + (size_t)M * hidden;

@@ -20,7 +20,9 @@
  *     asynchronous on it and perform no host synchronisation.
  *   - Device pointers must come from hipMalloc (or a torch CUDA tensor) on the current device
  *     and start on a 16-byte boundary (the kernels move 16 bytes a lane); a misaligned buffer
- *     is refused with W4A16_ERR_CONFIG before anything is launched.
+ *     is refused with W4A16_ERR_CONFIG before anything is launched. So is an output or
+ *     workspace that overlaps a buffer the same call reads while writing it (plan F2's
+ *     sublayer may alias its output exactly).
  *   - Compute calls that overlap in time on one device must be ordered on one stream: the
  *     split-K kernels of the small-M path share one per-device scratch buffer. The first call
  *     of a shape may grow that buffer (an allocation and a device synchronisation), so make it

@@ -211,3 +211,24 @@ def test_device_entries_refuse_misaligned_buffers_without_touching_the_device():
     assert st == w4a16.W4A16_ERR_CONFIG and "16-byte aligned" in w4a16.last_error()
     st = w4a16.lib.w4a16_tile_pack_device(8, 256, 0, base, base + 2, base, base, None)
     assert st == w4a16.W4A16_ERR_CONFIG and "16-byte aligned" in w4a16.last_error()
+
+
+def test_device_entries_refuse_overlapping_buffers_without_touching_the_device():
+    """An output that overlaps an input the same launch reads is refused before any launch;
+    plan F2's sublayer may alias its output exactly (the reference's layer_out)."""
+    base = 1 << 24
+    lib = w4a16.lib
+    st = lib.gemm_int4_bf16(base, base + (1 << 20), base + (1 << 21), base + 256, 2, 64, 256, 128,
+                            None)
+    assert st == w4a16.W4A16_ERR_CONFIG and "overlaps" in w4a16.last_error()
+    m, h, i = 2, 256, 512
+    res, sub, nw, out, ws = base, base + 4096, base + 8192, base + 12288, base + 16384
+    gup, gus, dnp, dns = base + (1 << 20), base + (2 << 20), base + (3 << 20), base + (4 << 20)
+    st = lib.mlp_int4_residual_norm_bf16(res, sub, nw, 1, 1e-6, gup, gus, dnp, dns, res, ws,
+                                         m, h, i, None)
+    assert st == w4a16.W4A16_ERR_CONFIG and "overlaps the residual" in w4a16.last_error()
+    st = lib.mlp_int4_residual_norm_bf16(res, sub, nw, 1, 1e-6, gup, gus, dnp, dns, out, res,
+                                         m, h, i, None)
+    assert st == w4a16.W4A16_ERR_CONFIG and "workspace overlaps" in w4a16.last_error()
+    st = lib.mlp_int4_norm_bf16(res, nw, 1, 1e-6, gup, gus, dnp, dns, ws + 64, ws, m, h, i, None)
+    assert st == w4a16.W4A16_ERR_CONFIG and "workspace overlaps" in w4a16.last_error()
