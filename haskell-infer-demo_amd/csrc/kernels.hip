@@ -134,6 +134,12 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
     return __builtin_bit_cast(uint4, v);
 }
 
+/* A weight piece: read once per call, so the load carries the non-temporal hint. */
+__device__ __forceinline__ uint4 buf_load16_stream(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2);
+    return __builtin_bit_cast(uint4, v);
+}
+
 __device__ __forceinline__ uint16_t buf_load_u16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
 }
@@ -219,7 +225,7 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
         const int p = ks + i * SK;
         const int g = 2 * p + half;
         const bool ok = p < P && g < G;
-        buf[i] = buf_load16(wr, ok ? (uint32_t)(g * 512 + piece * 16) : kOob);
+        buf[i] = buf_load16_stream(wr, ok ? (uint32_t)(g * 512 + piece * 16) : kOob);
         sbits[i] = buf_load_u16(sr, ok ? (uint32_t)(g * 16 + r * 2) : kOob);
     }
 
@@ -405,7 +411,7 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
         const int p = gw + i * kStride;
         const int g = 2 * p + half;
         const bool ok = p < P && g < G;
-        buf[i] = buf_load16(wr, ok ? (uint32_t)(g * 512 + piece * 16) : kOob);
+        buf[i] = buf_load16_stream(wr, ok ? (uint32_t)(g * 512 + piece * 16) : kOob);
         sbits[i] = buf_load_u16(sr, ok ? (uint32_t)(g * 16 + r * 2) : kOob);
     }
 
@@ -562,7 +568,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
     for (int i = 0; i < kGMax; ++i) {
         const bool ok = tile_ok && i < ng;
         const uint32_t unit = (uint32_t)(tile * G + g0 + i);
-        buf[i] = buf_load16(wr, ok ? (unit * 32 + q * 8 + r) * 16 : kOob);
+        buf[i] = buf_load16_stream(wr, ok ? (unit * 32 + q * 8 + r) * 16 : kOob);
         sbits[i] = buf_load_u16(sr, ok ? (unit * 8 + r) * 2 : kOob);
     }
 
@@ -789,7 +795,7 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
         const int p = ks + i * SK;
         const int g = 2 * p + a;
         const bool ok = p < P && g < G;
-        buf[i] = buf_load16(wr, ok ? (uint32_t)(g * 512 + (q * 8 + r) * 16) : kOob);
+        buf[i] = buf_load16_stream(wr, ok ? (uint32_t)(g * 512 + (q * 8 + r) * 16) : kOob);
         sbits[i] = buf_load_u16(sr, ok ? (uint32_t)(g * 16 + r * 2) : kOob);
     }
 
@@ -966,7 +972,7 @@ __global__ __launch_bounds__(1024) void gemv_rows16_kernel(
         const int g = ks + i * SK;
         const bool ok = tile_ok && g < G;
         const uint32_t unit = (uint32_t)(tile * G + g);
-        buf[i] = buf_load16(wr, ok ? unit * 512 + (uint32_t)(q * 8 + r) * 16 : kOob);
+        buf[i] = buf_load16_stream(wr, ok ? unit * 512 + (uint32_t)(q * 8 + r) * 16 : kOob);
         sbits[i] = buf_load_u16(sr, ok ? unit * 16 + (uint32_t)r * 2 : kOob);
     }
     __builtin_amdgcn_s_waitcnt(kVmcntWeights<NL>);
