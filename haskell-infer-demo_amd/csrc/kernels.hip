@@ -61,7 +61,6 @@ constexpr int kDppQuadSwap1 = 0xB1;      /* quad_perm [1,0,3,2]: lane ^ 1 */
 constexpr int kDppQuadSwap2 = 0x4E;      /* quad_perm [2,3,0,1]: lane ^ 2 */
 constexpr int kDppRowRor4 = 0x124;       /* row_ror:4 */
 constexpr int kDppRowRor8 = 0x128;       /* row_ror:8: lane ^ 8 within a row */
-constexpr int kDppRowHalfMirror = 0x141; /* lane 7 - l within each group of eight */
 constexpr int kDppRowShl4 = 0x104;       /* row_shl:4: lane l reads lane l + 4 of its row */
 
 template <int CTRL>
@@ -95,6 +94,47 @@ __device__ __forceinline__ float piece_dot(uint4 piece, const uint4 *xq, float x
         a = dot2_bf16(code_pair(w >> 5), xv.z, a);
         a = dot2_bf16(code_pair(w >> 9), xv.w, a);
     }
+    return fmaf(32.0f, a, -24.0f * xsum);
+}
+
+/* piece_dot with the activation taken from the lane's quad through DPP: quad lane s holds chunk
+ * s (x values 32 s' + 8 kb + j of the piece's group, s' = s) as four dwords, and every v_dot2c
+ * reads its activation operand from quad lane s by a quad_perm broadcast, so no activation passes
+ * through LDS. The compiler does not fold a DPP move into v_dot2c, hence the inline asm, and it
+ * cannot see the two hazards inside it: a VALU write of a register that a DPP operand reads
+ * needs two wait states before the first instruction (the leading s_nop 1), and a v_dot2c result
+ * needs a wait state before a following VALU instruction reads it (the trailing s_nop 1; without
+ * it the last product is lost, which the compiler guards against in its own code the same way).
+ * The accumulation order is piece_dot's, so the sum is bit-identical to it. */
+__device__ __forceinline__ float piece_dot_dpp(uint4 piece, uint4 xq, float xsum) {
+    const uint32_t w[4] = {piece.x, piece.y, piece.z, piece.w};
+    uint32_t c[16];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        c[4 * s] = code_pair(w[s] << 3);
+        c[4 * s + 1] = code_pair(w[s] >> 1);
+        c[4 * s + 2] = code_pair(w[s] >> 5);
+        c[4 * s + 3] = code_pair(w[s] >> 9);
+    }
+    float a = 0.0f;
+#define W4A16_DOT2_DPP(S, X, C)                                                                  \
+    "v_dot2c_f32_bf16_dpp %0, " X ", " C " quad_perm:[" S "," S "," S "," S "] row_mask:0xf "   \
+    "bank_mask:0xf\n"
+    asm volatile("s_nop 1\n"
+                 W4A16_DOT2_DPP("0", "%1", "%5") W4A16_DOT2_DPP("0", "%2", "%6")
+                 W4A16_DOT2_DPP("0", "%3", "%7") W4A16_DOT2_DPP("0", "%4", "%8")
+                 W4A16_DOT2_DPP("1", "%1", "%9") W4A16_DOT2_DPP("1", "%2", "%10")
+                 W4A16_DOT2_DPP("1", "%3", "%11") W4A16_DOT2_DPP("1", "%4", "%12")
+                 W4A16_DOT2_DPP("2", "%1", "%13") W4A16_DOT2_DPP("2", "%2", "%14")
+                 W4A16_DOT2_DPP("2", "%3", "%15") W4A16_DOT2_DPP("2", "%4", "%16")
+                 W4A16_DOT2_DPP("3", "%1", "%17") W4A16_DOT2_DPP("3", "%2", "%18")
+                 W4A16_DOT2_DPP("3", "%3", "%19") W4A16_DOT2_DPP("3", "%4", "%20")
+                 "s_nop 1\n"
+                 : "+v"(a)
+                 : "v"(xq.x), "v"(xq.y), "v"(xq.z), "v"(xq.w), "v"(c[0]), "v"(c[1]), "v"(c[2]),
+                   "v"(c[3]), "v"(c[4]), "v"(c[5]), "v"(c[6]), "v"(c[7]), "v"(c[8]), "v"(c[9]),
+                   "v"(c[10]), "v"(c[11]), "v"(c[12]), "v"(c[13]), "v"(c[14]), "v"(c[15]));
+#undef W4A16_DOT2_DPP
     return fmaf(32.0f, a, -24.0f * xsum);
 }
 
@@ -384,22 +424,19 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
     const int piece = lane & 31;
     const int kb = piece >> 3;
     const int r = piece & 7;
-    uint4 *xslice = smem4 + wave * NP * 32; /* pair i: 32 chunks of 16 bytes */
-    float *red = reinterpret_cast<float *>(smem4 + SK * NP * 32);
+    float *red = reinterpret_cast<float *>(smem4);
 
     /* 1. this wave's activation, then its weight pieces and scales. Pair p holds values
-     * [256 p, 256 p + 256) as 32 chunks of 8; the eight lanes 8 (4 half + kb) + j load the
-     * halves of the chunks c = 16 half + 4 s + kb (s = j >> 1, half j & 1), the 32 values that
-     * the pieces (half, kb, r) of those same lanes multiply. */
+     * [256 p, 256 p + 256) as 32 chunks of 8; a quad of lanes (same half and kb, lane & 3 = s)
+     * loads the chunks c = 16 half + 4 s + kb, the 32 values that each piece (half, kb, r) of
+     * the quad multiplies (the quads r < 4 and r >= 4 load the same chunks). */
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)K * 2);
-    const int xslot = (16 * half + 4 * ((lane & 7) >> 1) + kb) * 2 + (lane & 1); /* 8-byte slot */
-    uint2 xv[NP];
+    const int xchunk = 16 * half + 4 * (lane & 3) + kb;
+    uint4 xv[NP];
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
         const int p = gw + i * kStride;
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(
-            xr, p < P ? (int)(p * 512 + xslot * 8) : (int)kOob, 0, 0);
-        xv[i] = __builtin_bit_cast(uint2, v);
+        xv[i] = buf_load16(xr, p < P ? (uint32_t)(p * 512 + xchunk * 16) : kOob);
     }
     const size_t tile_bytes = (size_t)G * 512;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wt + (size_t)tile * tile_bytes, (uint32_t)tile_bytes);
@@ -415,22 +452,23 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
         sbits[i] = buf_load_u16(sr, ok ? (uint32_t)(g * 16 + r * 2) : kOob);
     }
 
-    /* 2. per pair: stage into the wave's slice, sums per (group, kb), dot products */
+    /* 2. per pair: the (half, kb) activation sum over the quad (two DPP adds), then the dot
+     * products with the activation broadcast from the quad's lanes */
     float acc = 0.0f;
-    uint2 *xs2 = reinterpret_cast<uint2 *>(xslice);
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-        if (gw + i * kStride < P) { /* wave-uniform */
-            xs2[i * 64 + xslot] = xv[i];
-            /* the (half, kb) sum over the lane's group of eight: three DPP adds */
-            float s4 = bf16_widen((uint16_t)(xv[i].x & 0xFFFFu)) + bf16_widen((uint16_t)(xv[i].x >> 16)) +
-                       bf16_widen((uint16_t)(xv[i].y & 0xFFFFu)) + bf16_widen((uint16_t)(xv[i].y >> 16));
-            s4 += dpp_f32<kDppQuadSwap1>(s4);
-            s4 += dpp_f32<kDppQuadSwap2>(s4);
-            const float xsum = s4 + dpp_f32<kDppRowHalfMirror>(s4);
-            const uint4 *xq = xslice + i * 32 + 16 * half + kb;
-            const uint4 xrow[4] = {xq[0], xq[4], xq[8], xq[12]};
-            acc = fmaf(piece_dot(buf[i], xrow, xsum), bf16_widen(sbits[i]), acc);
+        if (gw + i * kStride < P) { /* wave-uniform: every lane of the wave takes part */
+            const uint32_t xw[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+            float h[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                h[q] = bf16_widen((uint16_t)(xw[2 * q] & 0xFFFFu)) + bf16_widen((uint16_t)(xw[2 * q] >> 16)) +
+                       bf16_widen((uint16_t)(xw[2 * q + 1] & 0xFFFFu)) +
+                       bf16_widen((uint16_t)(xw[2 * q + 1] >> 16));
+            float s8 = h[0] + h[1];
+            s8 += dpp_f32<kDppQuadSwap1>(s8);
+            const float xsum = s8 + dpp_f32<kDppQuadSwap2>(s8);
+            acc = fmaf(piece_dot_dpp(buf[i], xv[i], xsum), bf16_widen(sbits[i]), acc);
         }
     }
 
@@ -489,7 +527,7 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
     }
 }
 
-size_t xwave_smem(int waves, int np) { return (size_t)waves * np * 512 + (size_t)waves * 32; }
+size_t xwave_smem(int waves, int np) { return (void)np, (size_t)waves * 32; }
 constexpr int kXwaveWaves = 16;
 
 
