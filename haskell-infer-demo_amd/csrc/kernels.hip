@@ -5,9 +5,10 @@
  * GEMVs: each lane loads one 16-byte piece (32 codes of one row) per step with a single
  * buffer_load_dwordx4, turns each pair of codes into a BF16 pair with a shift and one
  * v_bitop3_b32 (value 0.5 + u/32, u = nibble ^ 8 = code + 8, exact in BF16), and accumulates with
- * the packed BF16 dot product v_dot2_f32_bf16 against the activation pair. Since code = 32 v - 24,
+ * the packed BF16 dot product v_dot2c_f32_bf16 against the activation pair, whose activation
+ * operand is broadcast over DPP from the lane of its quad that holds it. Since code = 32 v - 24,
  * a piece's contribution is 32 * dot(v, x) - 24 * sum(x), with the per-piece activation sums
- * formed once when the activation is staged in LDS. The group's BF16 scale multiplies each
+ * formed by DPP adds (or once when the activation is staged in LDS). The group's BF16 scale multiplies each
  * piece's FP32 partial (the association of the reference's tiled kernel,
  * csrc/kernels/gemm_quant.cu:130-142). Lanes of one row are reduced with DPP moves within rows
  * of 16 lanes and shuffles across them.
@@ -15,8 +16,8 @@
  *   gemv_tiles_kernel   M = 1, block-staged activation (gate/up with the fused SiLU x up
  *                       epilogue, short-K linears); optional RMSNorm (and residual) prologue
  *   gemv_xwave_kernel   M = 1, long K (the down projection) and K = 1792..3072 (with the
- *                       fused SiLU x up epilogue for gate/up): wave-local activation slices;
- *                       optional residual epilogue
+ *                       fused SiLU x up epilogue for gate/up): each wave loads only its own
+ *                       pairs' activation, no LDS before the reduction; optional residual epilogue
  *   gemv_rows_kernel    2 <= M <= 8: the GEMV's block structure on v_mfma_f32_16x16x32_bf16 with
  *                       a block-diagonal operand, activation loaded straight into LDS
  *   gemv_rows16_kernel  9 <= M <= 16, short K: the same with a tile pair a wave
@@ -49,11 +50,6 @@ constexpr int kMaxRowK = 49152;   /* M = 1: the reference's limit (K * 2 <= 96 K
 constexpr int kMaxAnyK = 1 << 20; /* M > 1 (the MFMA form stages only its K range) */
 constexpr size_t kMaxLds = 163840; /* LDS a block can allocate on gfx950 */
 
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                           __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
 /* Cross-lane moves on the DPP path (a VALU operand modifier, no LDS round trip). quad_perm
  * patterns permute within groups of four lanes, row_ror:n rotates within rows of sixteen, and
  * row_half_mirror reverses each group of eight. */
@@ -80,32 +76,18 @@ __device__ __forceinline__ uint32_t code_pair(uint32_t shifted) {
     return (shifted & 0x00780078u) ^ 0x3F403F40u;
 }
 
-/* sum_{j<32} code_j * x_j for one 16-byte piece: 32 * dot(v, x) - 24 * xsum (one dependent
- * v_dot2 chain: the accumulator forwards, so splitting it only adds combining work). */
-__device__ __forceinline__ float piece_dot(uint4 piece, const uint4 *xq, float xsum) {
-    const uint32_t words[4] = {piece.x, piece.y, piece.z, piece.w};
-    float a = 0.0f;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        const uint32_t w = words[s];
-        const uint4 xv = xq[s];
-        a = dot2_bf16(code_pair(w << 3), xv.x, a);
-        a = dot2_bf16(code_pair(w >> 1), xv.y, a);
-        a = dot2_bf16(code_pair(w >> 5), xv.z, a);
-        a = dot2_bf16(code_pair(w >> 9), xv.w, a);
-    }
-    return fmaf(32.0f, a, -24.0f * xsum);
-}
-
-/* piece_dot with the activation taken from the lane's quad through DPP: quad lane s holds chunk
- * s (x values 32 s' + 8 kb + j of the piece's group, s' = s) as four dwords, and every v_dot2c
- * reads its activation operand from quad lane s by a quad_perm broadcast, so no activation passes
- * through LDS. The compiler does not fold a DPP move into v_dot2c, hence the inline asm, and it
+/* sum_{j<32} code_j * x_j for one 16-byte piece (row r, k block kb of a group): 32 * dot(v, x) -
+ * 24 * xsum, with v = 0.75 + code/32 from the unpack above and xsum the sum of the 32 x values.
+ * The activation comes from the lane's quad through DPP: quad lane s holds the 8 values
+ * 32 s + 8 kb + (0..7) of the group as four dwords, and every v_dot2c reads its activation
+ * operand from quad lane s by a quad_perm broadcast, so no lane needs more than its own 16 bytes
+ * of activation. The 16 products form one dependent v_dot2c chain in the order (s, dword) (the
+ * accumulator forwards, so splitting it only adds combining work). The compiler does not fold a DPP move into v_dot2c, hence the inline asm, and it
  * cannot see the two hazards inside it: a VALU write of a register that a DPP operand reads
  * needs two wait states before the first instruction (the leading s_nop 1), and a v_dot2c result
  * needs a wait state before a following VALU instruction reads it (the trailing s_nop 1; without
  * it the last product is lost, which the compiler guards against in its own code the same way).
- * The accumulation order is piece_dot's, so the sum is bit-identical to it. */
+ * The sum is bit-identical to the same chain written in plain HIP with the activation in LDS. */
 __device__ __forceinline__ float piece_dot_dpp(uint4 piece, uint4 xq, float xsum) {
     const uint32_t w[4] = {piece.x, piece.y, piece.z, piece.w};
     uint32_t c[16];
@@ -355,9 +337,10 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
     for (int i = 0; i < NL; ++i) {
         if (ks + i * SK < P) { /* wave-uniform */
             const int g = min(2 * (ks + i * SK) + half, G - 1);
-            const uint4 *xq = smem4 + g * 16 + kb;
-            const uint4 xrow[4] = {xq[0], xq[4], xq[8], xq[12]};
-            acc = fmaf(piece_dot(buf[i], xrow, xsum[4 * g + kb]), bf16_widen(sbits[i]), acc);
+            /* one 16-byte chunk a lane: quad lane s reads chunk 4 s + kb of group g, and the
+             * dot products take it from there over DPP */
+            const uint4 xq = smem4[g * 16 + 4 * (lane & 3) + kb];
+            acc = fmaf(piece_dot_dpp(buf[i], xq, xsum[4 * g + kb]), bf16_widen(sbits[i]), acc);
         }
     }
 
