@@ -65,6 +65,25 @@ __device__ __forceinline__ float dpp_f32(float v) {
         float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+/* v + v[l ^ 16] and v + v[l ^ 32] over the wave, on every lane, by the gfx950 lane swaps
+ * (v_permlane16_swap_b32 exchanges the odd rows of sixteen lanes of its first operand with the
+ * even rows of its second, v_permlane32_swap_b32 the upper half of the first with the lower half
+ * of the second; both operands hold v, so the two results are the lane's value and its partner's).
+ * A VALU exchange instead of an LDS-crossbar shuffle; the sum is the same FP32 add as
+ * v + __shfl_xor(v, 16 or 32). Inline asm because the compiler builtin does not keep its two
+ * results apart when both operands are one value; the waits cover the hazards the compiler
+ * cannot see inside the asm. */
+__device__ __forceinline__ float lane_sum16(float v) {
+    float x = v, y = v;
+    asm volatile("s_nop 1\n v_permlane16_swap_b32 %0, %1\n s_nop 1" : "+v"(x), "+v"(y));
+    return x + y;
+}
+__device__ __forceinline__ float lane_sum32(float v) {
+    float x = v, y = v;
+    asm volatile("s_nop 1\n v_permlane32_swap_b32 %0, %1\n s_nop 1" : "+v"(x), "+v"(y));
+    return x + y;
+}
+
 /* Code pairs as BF16. In a tile word the pair (j = 2q, 2q+1) sits at bits 4q and 16 + 4q, so one
  * shift puts both nibbles at bits 3-6 of their 16-bit halves and one v_bitop3_b32 computes
  * (s & 0x00780078) ^ 0x3F403F40: it keeps the two nibbles, flips their sign bits (u = code + 8)
@@ -346,8 +365,7 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
 
     /* 5. lanes r, r+8, ..., r+56 hold row r's partials; then the SK waves of a tile */
     acc += dpp_f32<kDppRowRor8>(acc);
-    acc += __shfl_xor(acc, 16);
-    acc += __shfl_xor(acc, 32);
+    acc = lane_sum32(lane_sum16(acc));
     float row_sum = acc;
     if (SK > 1) {
         if (lane < 8) red[wave * 8 + lane] = acc;
@@ -457,8 +475,7 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
 
     /* 3. lanes r, r+8, ..., r+56 hold row r's partials; then the SK waves of the block */
     acc += dpp_f32<kDppRowRor8>(acc);
-    acc += __shfl_xor(acc, 16);
-    acc += __shfl_xor(acc, 32);
+    acc = lane_sum32(lane_sum16(acc));
     if (lane < 8) red[wave * 8 + lane] = acc;
     __syncthreads();
     if (wave != 0 || lane >= 8) return;
