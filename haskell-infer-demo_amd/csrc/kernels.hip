@@ -21,6 +21,9 @@
  *   gemv_rows_kernel    2 <= M <= 8: the GEMV's block structure on v_mfma_f32_16x16x32_bf16 with
  *                       a block-diagonal operand, activation loaded straight into LDS
  *   gemv_rows16_kernel  9 <= M <= 16, short K: the same with a tile pair a wave
+ *   gemv_rows16x_kernel 8 <= M <= 15, long K, no pair: a tile pair a block, each lane loading
+ *                       its MFMA A operand from memory into registers (no LDS staging, no K
+ *                       split across blocks)
  *   mfma_gemm_kernel    2 <= M <= 16 where the above do not fit: v_mfma_f32_16x16x32_bf16, K
  *                       split across blocks
  *   rmsnorm_kernel, residual_add_kernel, silu_mul_packed_kernel: the norm, the residual update
@@ -1074,6 +1077,115 @@ __global__ __launch_bounds__(1024) void gemv_rows16_kernel(
     }
 }
 
+/* Up to 16 rows, long K, no PAIR: one tile pair a block of 16 waves, wave ks taking groups
+ * ks + 16 i, and every lane loading its own MFMA A operand (row n, the 8 values of k block q
+ * of each 32-wide slice) straight from memory into registers instead of staging the rows in
+ * LDS. The A bytes of a block are M K 2 (from L2: every block reads the same rows), against
+ * 16 K / 2 bytes of weight, but nothing is shared across the waves of a block, so no LDS pass
+ * or block barrier stands before the MFMAs and no K split crosses blocks: the 16 waves meet
+ * in LDS once, at the end. Suits the down projection (N small, K long), where the LDS-staged
+ * rows no longer fit and splitting K across blocks costs a combine through the coherence
+ * point. The weight loads of every group are issued first, then the A loads, kept D groups
+ * ahead of the MFMAs. Lanes of A rows >= M load zeros (no memory traffic). */
+template <bool OUT_F32, int NL, int D>
+__global__ __launch_bounds__(1024) void gemv_rows16x_kernel(
+    const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K,
+    uint16_t *residual) {
+    constexpr int SK = 16;
+    __shared__ f32x4_t red[SK * 64];
+    const int G = K >> 7;
+    const int tiles = N >> 3;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int ks = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tp = blockIdx.x;
+    const int q = lane >> 4;
+    const int n = lane & 15;
+    const int r = n & 7;
+    const int tile = 2 * tp + (n >> 3);
+
+    /* 1. every weight piece and scale of this wave (a tile past N reads zeros) */
+    const bool tile_ok = tile < tiles;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wt, (uint32_t)((size_t)N * K / 2));
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(st, (uint32_t)((size_t)N * G * 2));
+    uint4 buf[NL];
+    uint16_t sbits[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int g = ks + i * SK;
+        const bool ok = tile_ok && g < G;
+        const uint32_t unit = (uint32_t)(tile * G + g);
+        buf[i] = buf_load16_stream(wr, ok ? unit * 512 + (uint32_t)(q * 8 + r) * 16 : kOob);
+        sbits[i] = buf_load_u16(sr, ok ? unit * 16 + (uint32_t)r * 2 : kOob);
+    }
+
+    /* 2. the A operands of group i: for MFMA t, row n, k = 128 g + 32 t + 8 q .. + 7 */
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)M * K * 2);
+    const bool row_ok = n < M;
+    const uint32_t row_off = (uint32_t)(n * K + q * 8) * 2;
+    uint4 av[D][4];
+    auto load_a = [&](int i) {
+        const int g = ks + i * SK;
+        const bool ok = row_ok && g < G;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            av[i % D][t] = buf_load16(xr, ok ? row_off + (uint32_t)(g * 128 + 32 * t) * 2 : kOob);
+    };
+#pragma unroll
+    for (int i = 0; i < D && i < NL; ++i) load_a(i);
+
+    /* 3. eight MFMAs a group (the offset ones as in gemv_rows_kernel) */
+    const uint4 offs = make_uint4(0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u);
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        if (ks + i * SK < G) { /* wave-uniform */
+            const uint32_t words[4] = {buf[i].x, buf[i].y, buf[i].z, buf[i].w};
+            f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const bf16x8_t a = __builtin_bit_cast(bf16x8_t, av[i % D][t]);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, unpack8(words[t]), d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, offs),
+                                                            d, 0, 0, 0);
+            }
+            const float sc = bf16_widen(sbits[i]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = fmaf(sc, d[j], acc[j]);
+        }
+        if (i + D < NL) load_a(i + D);
+    }
+
+    /* 4. the 16 waves in LDS, summed in wave order; lane (n, q) holds rows 4 q + j of column n */
+    red[ks * 64 + lane] = acc;
+    __syncthreads();
+    if (ks != 0) return;
+    f32x4_t sum = acc;
+#pragma unroll
+    for (int w = 1; w < SK; ++w) {
+        const f32x4_t v = red[w * 64 + lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sum[j] += v[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float row_sum = 32.0f * sum[j];
+        const int m = 4 * q + j;
+        if (m < M && tile_ok) {
+            const size_t o = (size_t)m * N + tile * 8 + r;
+            if (OUT_F32) {
+                reinterpret_cast<float *>(out)[o] = row_sum;
+            } else {
+                const uint16_t ob = bf16_rne(row_sum);
+                /* plan F2: the residual, already BF16(residual + sublayer), gains the output */
+                if (residual) residual[o] = (uint16_t)(bf16_add2(residual[o], ob) & 0xFFFFu);
+                reinterpret_cast<uint16_t *>(out)[o] = ob;
+            }
+        }
+    }
+}
+
 /* RMSNorm of each row (one block a row): BF16(x * rsqrt(sum x^2 / cols + eps) * (bias + w)),
  * FP32 arithmetic (reference csrc/kernels/flashinfer_norm.cu:22-76). Each thread holds CH
  * 8-value chunks of the row, all loaded before any use, so a row costs one load round trip;
@@ -1445,6 +1557,32 @@ int launch_rows16_nl(const uint16_t *x, int M, const uint8_t *w, const uint16_t 
 
 int device_cus();
 
+template <bool OUT_F32, int NL>
+int launch_rows16x_nl(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
+                      int N, int K, hipStream_t stream, uint16_t *residual) {
+    constexpr int D = NL <= 5 ? NL : NL <= 9 ? 4 : 3;
+    const int pairs = (N / 8 + 1) / 2;
+    hipLaunchKernelGGL((gemv_rows16x_kernel<OUT_F32, NL, D>), dim3(pairs), dim3(1024), 0, stream,
+                       x, M, w, s, out, N, K, residual);
+    return hip_status(hipGetLastError(), "gemv rows16x launch");
+}
+
+/* Long-K rows without LDS staging (gemv_rows16x_kernel): one tile pair a block of 16 waves. */
+template <bool OUT_F32>
+int launch_rows16x(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
+                   int K, hipStream_t stream, uint16_t *residual = nullptr) {
+    const int nl = (K / 128 + 15) / 16;
+    if (nl <= 2) return launch_rows16x_nl<OUT_F32, 2>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 3) return launch_rows16x_nl<OUT_F32, 3>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 4) return launch_rows16x_nl<OUT_F32, 4>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 5) return launch_rows16x_nl<OUT_F32, 5>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 6) return launch_rows16x_nl<OUT_F32, 6>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 8) return launch_rows16x_nl<OUT_F32, 8>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 9) return launch_rows16x_nl<OUT_F32, 9>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 12) return launch_rows16x_nl<OUT_F32, 12>(x, M, w, s, out, N, K, stream, residual);
+    return 1;
+}
+
 template <bool PAIR, bool OUT_F32>
 int launch_rows16(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
                   int K, hipStream_t stream) {
@@ -1465,6 +1603,13 @@ template <bool PAIR, bool OUT_F32>
 int launch_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
                 int K, hipStream_t stream, const NormArgs *norm = nullptr,
                 uint16_t *residual = nullptr) {
+    /* long K (the staged rows would not fit LDS): registers-fed A from M = 8 (9 with the
+     * residual epilogue) to 15; at 16 the split-K MFMA form is faster. C1 down, medians of
+     * interleaved whole-call runs, split-K or LDS-staged against rows16x: M = 8 20.5 / 19.9 us,
+     * 10 22.7 / 21.0, 13 23.9 / 22.6, 14 24.2 / 23.4, 15 24.2 / 23.9, 16 24.4 / 24.6; at M = 8
+     * plan F2 23.3 against 23.6, and M = 4 and 6 tie. */
+    if (!PAIR && !norm && M >= (residual ? 9 : 8) && M <= 15 && rows16_smem(M, K, 16) > kMaxLds)
+        return launch_rows16x<OUT_F32>(x, M, w, s, out, N, K, stream, residual);
     if (M > 8 && M <= 16 && !norm && !residual)
         return launch_rows16<PAIR, OUT_F32>(x, M, w, s, out, N, K, stream);
     if (M < 2 || M > 8) return 1;

@@ -135,14 +135,15 @@ def test_small_m_parity(cuda, m):
     assert_parity(out, oracle.gemm_bf16(x, p, s, n, k), f"gemm M={m}")
 
 
-@pytest.mark.parametrize("m", [2, 3, 4, 5, 6, 7, 8, 9, 12, 16])
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 6, 7, 8, 9, 12, 15, 16])
 def test_few_rows_parity(cuda, m):
     """2 <= M <= 16 on the few-row MFMA kernels, through each of their block shapes: 1 group
     pair, an odd group count with a half-filled block of tiles (and, from M = 9, a tile pair
-    missing its second tile), 10, 13 (odd) and 38 pairs; the last takes the split-K MFMA form
-    from M = 9 (its staged rows would pass a block's LDS). The gate/up pair with the fused SiLU
-    epilogue at an odd group count."""
-    for n, k in [(256, 256), (24, 1152), (2560, 2560), (64, 3200), (640, 9728)]:
+    missing its second tile), 10, 13 (odd), 38 and 68 pairs; the last two take the registers-fed
+    long-K kernel from M = 8 to 15 (at 68 pairs with its A loads kept 4 groups ahead of the
+    MFMAs) and the split-K MFMA form at M = 16 (their staged rows would pass a block's LDS). The
+    gate/up pair with the fused SiLU epilogue at an odd group count."""
+    for n, k in [(256, 256), (24, 1152), (2560, 2560), (64, 3200), (640, 9728), (64, 17408)]:
         say(f"gemm M={m} n={n} k={k}")
         p, s = make_weight(n, k, seed=n + k + m)
         x = oracle.synth_activation(m, k, seed=200 + m)
@@ -438,9 +439,10 @@ def test_norm_prologue_shapes(cuda, hidden):
 
 
 @pytest.mark.parametrize("style", [0, 1])
-@pytest.mark.parametrize("m", [1, 2, 16])
+@pytest.mark.parametrize("m", [1, 2, 12, 16])
 def test_ffn_residual_norm_parity(cuda, style, m):
-    """Plan F2 around the MLP (reference csrc/layer_dispatch.cu:183-209): the layer output
+    """Plan F2 around the MLP (reference csrc/layer_dispatch.cu:183-209), with the residual added
+    in each down kernel's epilogue (M = 12: the registers-fed long-K kernel): the layer output
     against the oracle (residual update, norm, FFN) at the end-to-end bar, and the updated
     residual BF16(BF16(r + s) + out) bit-exact given the kernel's own output; at M = 1 and 2 (the
     two-launch forms) also with the sublayer aliasing the output buffer, as the reference's
