@@ -21,9 +21,11 @@
  *   gemv_rows_kernel    2 <= M <= 8: the GEMV's block structure on v_mfma_f32_16x16x32_bf16 with
  *                       a block-diagonal operand, activation loaded straight into LDS
  *   gemv_rows16_kernel  9 <= M <= 16, short K: the same with a tile pair a wave
- *   gemv_rows16x_kernel 8 <= M <= 15, long K, no pair: a tile pair a block, each lane loading
- *                       its MFMA A operand from memory into registers (no LDS staging, no K
- *                       split across blocks)
+ *   gemv_rows16x_kernel long K, no pair (the down projection): a tile pair a block, each lane
+ *                       loading its MFMA A operand from memory into registers (no LDS staging,
+ *                       no K split across blocks); 4 <= M <= 16 inside the FFN entry points,
+ *                       which keep the intermediate chunk-major for it, 8 <= M <= 15 on
+ *                       row-major rows in gemm_int4_bf16
  *   mfma_gemm_kernel    2 <= M <= 16 where the above do not fit: v_mfma_f32_16x16x32_bf16, K
  *                       split across blocks
  *   rmsnorm_kernel, residual_add_kernel, silu_mul_packed_kernel: the norm, the residual update
@@ -156,6 +158,13 @@ __device__ __forceinline__ float silu_f32(float g) {
 
 __device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
     return bf16_rne(silu_f32(gate) * up);
+}
+
+/* Index of element (m, i) of an M x cols activation: row-major, or (cm) chunk-major, i.e.
+ * [cols / 8 chunks][M rows][8 values], where one 16-byte chunk of every row sits together, so
+ * the MFMA A operands of all rows at one k block are contiguous in memory. */
+__device__ __forceinline__ size_t act_index(int m, int i, int M, int cols, int cm) {
+    return cm ? ((size_t)(i >> 3) * M + m) * 8 + (i & 7) : (size_t)m * cols + i;
 }
 
 /* Two packed BF16 sums, each BF16(f32(a) + f32(b)) (the residual update of reference
@@ -570,7 +579,7 @@ template <int OUT, int XPRE, int MI>
 __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
     const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, int S, int GS,
-    float *__restrict__ partial, unsigned *__restrict__ counters, uint16_t *residual) {
+    float *__restrict__ partial, unsigned *__restrict__ counters, uint16_t *residual, int cm) {
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
     const int tiles = N >> 3;
@@ -729,7 +738,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
             if (r < 4 && m < M && tile < tiles) {
                 const float gate = bf16_widen(bf16_rne(acc[i]));
                 const float up = bf16_widen(bf16_rne(upv));
-                reinterpret_cast<uint16_t *>(out)[(size_t)m * inter + tile * 4 + r] =
+                reinterpret_cast<uint16_t *>(out)[act_index(m, tile * 4 + r, M, inter, cm)] =
                     silu_mul_bf16(gate, up);
             }
         }
@@ -774,7 +783,7 @@ template <bool PAIR, bool OUT_F32, int TB, int SK, int NL, int MI, bool NORM = f
 __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
     const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K,
-    const uint16_t *__restrict__ norm_w, float norm_bias, float eps, uint16_t *residual) {
+    const uint16_t *__restrict__ norm_w, float norm_bias, float eps, uint16_t *residual, int cm) {
     constexpr int W = TB * SK;
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
@@ -945,7 +954,7 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
         if (r < 4 && m < M) {
             const float gate = bf16_widen(bf16_rne(row_sum));
             const float up = bf16_widen(bf16_rne(upv));
-            reinterpret_cast<uint16_t *>(out)[(size_t)m * (N >> 1) + tile * 4 + r] =
+            reinterpret_cast<uint16_t *>(out)[act_index(m, tile * 4 + r, M, N >> 1, cm)] =
                 silu_mul_bf16(gate, up);
         }
     } else if (m < M) {
@@ -970,7 +979,7 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
 template <bool PAIR, bool OUT_F32, int NL>
 __global__ __launch_bounds__(1024) void gemv_rows16_kernel(
     const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
-    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, int TP, int SK) {
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, int TP, int SK, int cm) {
     const int W = TP * SK;
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
@@ -1064,7 +1073,7 @@ __global__ __launch_bounds__(1024) void gemv_rows16_kernel(
             if (r < 4 && m < M && tile_ok) {
                 const float gate = bf16_widen(bf16_rne(row_sum));
                 const float up = bf16_widen(bf16_rne(upv));
-                reinterpret_cast<uint16_t *>(out)[(size_t)m * (N >> 1) + tile * 4 + r] =
+                reinterpret_cast<uint16_t *>(out)[act_index(m, tile * 4 + r, M, N >> 1, cm)] =
                     silu_mul_bf16(gate, up);
             }
         } else if (m < M && tile_ok) {
@@ -1086,8 +1095,14 @@ __global__ __launch_bounds__(1024) void gemv_rows16_kernel(
  * in LDS once, at the end. Suits the down projection (N small, K long), where the LDS-staged
  * rows no longer fit and splitting K across blocks costs a combine through the coherence
  * point. The weight loads of every group are issued first, then the A loads, kept D groups
- * ahead of the MFMAs. Lanes of A rows >= M load zeros (no memory traffic). */
-template <bool OUT_F32, int NL, int D>
+ * ahead of the MFMAs. Lanes of A rows >= M load zeros (no memory traffic).
+ *
+ * With CM the activation is chunk-major ([K / 8 chunks][M rows][8 values], written so by the
+ * gate/up kernels inside the FFN entry points): the A operands of one MFMA are then 64 M
+ * contiguous bytes, M / 2 whole cache lines, where the row-major rows give 16 half lines. The
+ * A stream is what bounds this kernel (down at M = 16 without its A loads: 6.0 us against
+ * 13.1), and the chunk-major order takes it from 13.1 to 8.4 us. */
+template <bool OUT_F32, int NL, int D, bool CM>
 __global__ __launch_bounds__(1024) void gemv_rows16x_kernel(
     const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K,
@@ -1130,7 +1145,10 @@ __global__ __launch_bounds__(1024) void gemv_rows16x_kernel(
         const bool ok = row_ok && g < G;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-            av[i % D][t] = buf_load16(xr, ok ? row_off + (uint32_t)(g * 128 + 32 * t) * 2 : kOob);
+            av[i % D][t] = buf_load16(
+                xr, !ok ? kOob
+                    : CM ? (uint32_t)(((g * 16 + 4 * t + q) * M + n) * 16)
+                         : row_off + (uint32_t)(g * 128 + 32 * t) * 2);
     };
 #pragma unroll
     for (int i = 0; i < D && i < NL; ++i) load_a(i);
@@ -1503,7 +1521,7 @@ size_t rows_smem(int M, int K, int waves, bool norm = false) {
 template <bool PAIR, bool OUT_F32, int TB, int SK, int NL>
 int launch_rows_mi(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
                    int N, int K, hipStream_t stream, const NormArgs *norm = nullptr,
-                   uint16_t *residual = nullptr) {
+                   uint16_t *residual = nullptr, int cm = 0) {
     if (SK * NL < (K / 128 + 1) / 2)
         return set_error(W4A16_ERR_CONFIG, "internal: a %d x %d few-row shape covers %d of %d group pairs",
                          SK, NL, SK * NL, (K / 128 + 1) / 2);
@@ -1515,16 +1533,16 @@ int launch_rows_mi(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s
     const float nb = norm ? norm->bias : 0.0f, ne = norm ? norm->eps : 0.0f;
     if (M == 2 && norm)
         hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 2, true>), grid, block,
-                           smem, stream, x, M, w, s, out, N, K, nw, nb, ne, residual);
+                           smem, stream, x, M, w, s, out, N, K, nw, nb, ne, residual, cm);
     else if (M == 2)
         hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 2>), grid, block, smem,
-                           stream, x, M, w, s, out, N, K, nw, nb, ne, residual);
+                           stream, x, M, w, s, out, N, K, nw, nb, ne, residual, cm);
     else if (norm)
         hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 4, true>), grid, block,
-                           smem, stream, x, M, w, s, out, N, K, nw, nb, ne, residual);
+                           smem, stream, x, M, w, s, out, N, K, nw, nb, ne, residual, cm);
     else
         hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 4>), grid, block, smem,
-                           stream, x, M, w, s, out, N, K, nw, nb, ne, residual);
+                           stream, x, M, w, s, out, N, K, nw, nb, ne, residual, cm);
     return hip_status(hipGetLastError(), "gemv rows launch");
 }
 
@@ -1546,63 +1564,63 @@ size_t rows16_smem(int M, int K, int waves) {
 
 template <bool PAIR, bool OUT_F32, int NL>
 int launch_rows16_nl(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
-                     int N, int K, int TP, int SK, hipStream_t stream) {
+                     int N, int K, int TP, int SK, hipStream_t stream, int cm) {
     const size_t smem = rows16_smem(M, K, TP * SK);
     if (smem > kMaxLds) return 1;
     const int pairs = (N / 8 + 1) / 2;
     hipLaunchKernelGGL((gemv_rows16_kernel<PAIR, OUT_F32, NL>), dim3((pairs + TP - 1) / TP),
-                       dim3(TP * SK * 64), smem, stream, x, M, w, s, out, N, K, TP, SK);
+                       dim3(TP * SK * 64), smem, stream, x, M, w, s, out, N, K, TP, SK, cm);
     return hip_status(hipGetLastError(), "gemv rows16 launch");
 }
 
 int device_cus();
 
-template <bool OUT_F32, int NL>
+template <bool OUT_F32, bool CM, int NL>
 int launch_rows16x_nl(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
                       int N, int K, hipStream_t stream, uint16_t *residual) {
     constexpr int D = NL <= 5 ? NL : NL <= 9 ? 4 : 3;
     const int pairs = (N / 8 + 1) / 2;
-    hipLaunchKernelGGL((gemv_rows16x_kernel<OUT_F32, NL, D>), dim3(pairs), dim3(1024), 0, stream,
+    hipLaunchKernelGGL((gemv_rows16x_kernel<OUT_F32, NL, D, CM>), dim3(pairs), dim3(1024), 0, stream,
                        x, M, w, s, out, N, K, residual);
     return hip_status(hipGetLastError(), "gemv rows16x launch");
 }
 
 /* Long-K rows without LDS staging (gemv_rows16x_kernel): one tile pair a block of 16 waves. */
-template <bool OUT_F32>
+template <bool OUT_F32, bool CM = false>
 int launch_rows16x(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
                    int K, hipStream_t stream, uint16_t *residual = nullptr) {
     const int nl = (K / 128 + 15) / 16;
-    if (nl <= 2) return launch_rows16x_nl<OUT_F32, 2>(x, M, w, s, out, N, K, stream, residual);
-    if (nl <= 3) return launch_rows16x_nl<OUT_F32, 3>(x, M, w, s, out, N, K, stream, residual);
-    if (nl <= 4) return launch_rows16x_nl<OUT_F32, 4>(x, M, w, s, out, N, K, stream, residual);
-    if (nl <= 5) return launch_rows16x_nl<OUT_F32, 5>(x, M, w, s, out, N, K, stream, residual);
-    if (nl <= 6) return launch_rows16x_nl<OUT_F32, 6>(x, M, w, s, out, N, K, stream, residual);
-    if (nl <= 8) return launch_rows16x_nl<OUT_F32, 8>(x, M, w, s, out, N, K, stream, residual);
-    if (nl <= 9) return launch_rows16x_nl<OUT_F32, 9>(x, M, w, s, out, N, K, stream, residual);
-    if (nl <= 12) return launch_rows16x_nl<OUT_F32, 12>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 2) return launch_rows16x_nl<OUT_F32, CM, 2>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 3) return launch_rows16x_nl<OUT_F32, CM, 3>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 4) return launch_rows16x_nl<OUT_F32, CM, 4>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 5) return launch_rows16x_nl<OUT_F32, CM, 5>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 6) return launch_rows16x_nl<OUT_F32, CM, 6>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 8) return launch_rows16x_nl<OUT_F32, CM, 8>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 9) return launch_rows16x_nl<OUT_F32, CM, 9>(x, M, w, s, out, N, K, stream, residual);
+    if (nl <= 12) return launch_rows16x_nl<OUT_F32, CM, 12>(x, M, w, s, out, N, K, stream, residual);
     return 1;
 }
 
 template <bool PAIR, bool OUT_F32>
 int launch_rows16(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
-                  int K, hipStream_t stream) {
+                  int K, hipStream_t stream, int cm = 0) {
     const int G = K / 128;
     const int pairs = (N / 8 + 1) / 2;
     const int TP = std::min(16, (pairs + device_cus() - 1) / device_cus());
     const int SK = std::max(1, 16 / TP);
     const int nl = (G + SK - 1) / SK;
-    if (nl <= 2) return launch_rows16_nl<PAIR, OUT_F32, 2>(x, M, w, s, out, N, K, TP, SK, stream);
-    if (nl <= 4) return launch_rows16_nl<PAIR, OUT_F32, 4>(x, M, w, s, out, N, K, TP, SK, stream);
-    if (nl <= 6) return launch_rows16_nl<PAIR, OUT_F32, 6>(x, M, w, s, out, N, K, TP, SK, stream);
-    if (nl <= 8) return launch_rows16_nl<PAIR, OUT_F32, 8>(x, M, w, s, out, N, K, TP, SK, stream);
-    if (nl <= 12) return launch_rows16_nl<PAIR, OUT_F32, 12>(x, M, w, s, out, N, K, TP, SK, stream);
+    if (nl <= 2) return launch_rows16_nl<PAIR, OUT_F32, 2>(x, M, w, s, out, N, K, TP, SK, stream, cm);
+    if (nl <= 4) return launch_rows16_nl<PAIR, OUT_F32, 4>(x, M, w, s, out, N, K, TP, SK, stream, cm);
+    if (nl <= 6) return launch_rows16_nl<PAIR, OUT_F32, 6>(x, M, w, s, out, N, K, TP, SK, stream, cm);
+    if (nl <= 8) return launch_rows16_nl<PAIR, OUT_F32, 8>(x, M, w, s, out, N, K, TP, SK, stream, cm);
+    if (nl <= 12) return launch_rows16_nl<PAIR, OUT_F32, 12>(x, M, w, s, out, N, K, TP, SK, stream, cm);
     return 1;
 }
 
 template <bool PAIR, bool OUT_F32>
 int launch_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
                 int K, hipStream_t stream, const NormArgs *norm = nullptr,
-                uint16_t *residual = nullptr) {
+                uint16_t *residual = nullptr, int cm = 0) {
     /* long K (the staged rows would not fit LDS): registers-fed A from M = 8 (9 with the
      * residual epilogue) to 15; at 16 the split-K MFMA form is faster. C1 down, medians of
      * interleaved whole-call runs, split-K or LDS-staged against rows16x: M = 8 20.5 / 19.9 us,
@@ -1611,25 +1629,25 @@ int launch_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, v
     if (!PAIR && !norm && M >= (residual ? 9 : 8) && M <= 15 && rows16_smem(M, K, 16) > kMaxLds)
         return launch_rows16x<OUT_F32>(x, M, w, s, out, N, K, stream, residual);
     if (M > 8 && M <= 16 && !norm && !residual)
-        return launch_rows16<PAIR, OUT_F32>(x, M, w, s, out, N, K, stream);
+        return launch_rows16<PAIR, OUT_F32>(x, M, w, s, out, N, K, stream, cm);
     if (M < 2 || M > 8) return 1;
     const int pairs = (K / 128 + 1) / 2;
     if (pairs <= 12 && M <= 4) {
-        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 4, 1, 3>(x, M, w, s, out, N, K, stream, norm, residual);
-        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 3>(x, M, w, s, out, N, K, stream, norm, residual);
-        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 5>(x, M, w, s, out, N, K, stream, norm, residual);
-        return launch_rows_mi<PAIR, OUT_F32, 2, 2, 6>(x, M, w, s, out, N, K, stream, norm, residual);
+        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 4, 1, 3>(x, M, w, s, out, N, K, stream, norm, residual, cm);
+        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 3>(x, M, w, s, out, N, K, stream, norm, residual, cm);
+        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 5>(x, M, w, s, out, N, K, stream, norm, residual, cm);
+        return launch_rows_mi<PAIR, OUT_F32, 2, 2, 6>(x, M, w, s, out, N, K, stream, norm, residual, cm);
     }
     if (pairs <= 12) {
-        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 8, 1, 3>(x, M, w, s, out, N, K, stream, norm, residual);
-        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 3>(x, M, w, s, out, N, K, stream, norm, residual);
-        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 5>(x, M, w, s, out, N, K, stream, norm, residual);
-        return launch_rows_mi<PAIR, OUT_F32, 4, 2, 6>(x, M, w, s, out, N, K, stream, norm, residual);
+        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 8, 1, 3>(x, M, w, s, out, N, K, stream, norm, residual, cm);
+        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 3>(x, M, w, s, out, N, K, stream, norm, residual, cm);
+        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 5>(x, M, w, s, out, N, K, stream, norm, residual, cm);
+        return launch_rows_mi<PAIR, OUT_F32, 4, 2, 6>(x, M, w, s, out, N, K, stream, norm, residual, cm);
     }
-    if (pairs <= 20) return launch_rows_mi<PAIR, OUT_F32, 2, 4, 5>(x, M, w, s, out, N, K, stream, norm, residual);
-    if (pairs <= 40) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 5>(x, M, w, s, out, N, K, stream, norm, residual);
-    if (pairs <= 48) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 6>(x, M, w, s, out, N, K, stream, norm, residual);
-    if (pairs <= 80) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 10>(x, M, w, s, out, N, K, stream, norm, residual);
+    if (pairs <= 20) return launch_rows_mi<PAIR, OUT_F32, 2, 4, 5>(x, M, w, s, out, N, K, stream, norm, residual, cm);
+    if (pairs <= 40) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 5>(x, M, w, s, out, N, K, stream, norm, residual, cm);
+    if (pairs <= 48) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 6>(x, M, w, s, out, N, K, stream, norm, residual, cm);
+    if (pairs <= 80) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 10>(x, M, w, s, out, N, K, stream, norm, residual, cm);
     return 1;
 }
 
@@ -1728,26 +1746,26 @@ MfmaPlan plan_mfma(int M, int N, int K) {
 template <int OUT, int XPRE>
 int launch_mfma_x(const MfmaPlan &p, const uint16_t *x, int M, const uint8_t *w,
                   const uint16_t *s, void *out, int N, int K, float *partial, unsigned *counters,
-                  hipStream_t stream, uint16_t *residual) {
+                  hipStream_t stream, uint16_t *residual, int cm) {
     if (M == 1)
         hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE, 1>), dim3(p.grid), dim3(kMfmaWaves * 64),
                            p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters,
-                           residual);
+                           residual, cm);
     else if (M == 2)
         hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE, 2>), dim3(p.grid), dim3(kMfmaWaves * 64),
                            p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters,
-                           residual);
+                           residual, cm);
     else
         hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE, 4>), dim3(p.grid), dim3(kMfmaWaves * 64),
                            p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters,
-                           residual);
+                           residual, cm);
     return hip_status(hipGetLastError(), "mfma gemm launch");
 }
 
 /* M <= 16 rows of x against a tile-order weight. */
 template <int OUT>
 int launch_mfma(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
-                int K, hipStream_t stream, uint16_t *residual = nullptr) {
+                int K, hipStream_t stream, uint16_t *residual = nullptr, int cm = 0) {
     const MfmaPlan p = plan_mfma(M, N, K);
     float *partial = nullptr;
     unsigned *counters = nullptr;
@@ -1756,10 +1774,10 @@ int launch_mfma(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, v
         if (st) return st;
     }
     switch (p.xpre) {
-        case 1: return launch_mfma_x<OUT, 1>(p, x, M, w, s, out, N, K, partial, counters, stream, residual);
-        case 2: return launch_mfma_x<OUT, 2>(p, x, M, w, s, out, N, K, partial, counters, stream, residual);
-        case 4: return launch_mfma_x<OUT, 4>(p, x, M, w, s, out, N, K, partial, counters, stream, residual);
-        default: return launch_mfma_x<OUT, 8>(p, x, M, w, s, out, N, K, partial, counters, stream, residual);
+        case 1: return launch_mfma_x<OUT, 1>(p, x, M, w, s, out, N, K, partial, counters, stream, residual, cm);
+        case 2: return launch_mfma_x<OUT, 2>(p, x, M, w, s, out, N, K, partial, counters, stream, residual, cm);
+        case 4: return launch_mfma_x<OUT, 4>(p, x, M, w, s, out, N, K, partial, counters, stream, residual, cm);
+        default: return launch_mfma_x<OUT, 8>(p, x, M, w, s, out, N, K, partial, counters, stream, residual, cm);
     }
 }
 
@@ -1823,7 +1841,7 @@ int check_gemm_args(const void *a, const void *p, const void *s, const void *o, 
  * all rows; larger M runs on 16-row slices. */
 template <int OUT>
 static int run_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
-                    int N, int K, hipStream_t stream) {
+                    int N, int K, hipStream_t stream, int cm = 0) {
     constexpr bool PAIR = OUT == kOutPairSilu;
     constexpr bool F32 = OUT == kOutF32;
     const int out_cols = PAIR ? N / 2 : N;
@@ -1836,8 +1854,8 @@ static int run_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *
          * (then the MFMA form with one live row) */
         const bool gemv = rows == 1 && (!PAIR || K <= kMaxGemvK);
         int st = gemv ? launch_gemv<PAIR, F32>(xs, w, s, os, N, K, stream)
-                      : launch_rows<PAIR, F32>(xs, rows, w, s, os, N, K, stream);
-        if (st > 0) st = launch_mfma<OUT>(xs, rows, w, s, os, N, K, stream);
+                      : launch_rows<PAIR, F32>(xs, rows, w, s, os, N, K, stream, nullptr, nullptr, cm);
+        if (st > 0) st = launch_mfma<OUT>(xs, rows, w, s, os, N, K, stream, nullptr, cm);
         if (st) return st;
     }
     return W4A16_OK;
@@ -1862,6 +1880,16 @@ extern "C" int gate_up_silu_int4_bf16(const uint16_t *x, const uint8_t *gu_packe
                                   static_cast<hipStream_t>(stream));
 }
 
+/* Inside the FFN entry points the gate/up kernel writes the intermediate chunk-major for a
+ * down projection on gemv_rows16x_kernel<CM> when K is long (64 to 192 groups: at most 12 a
+ * wave) and 4 <= M <= 16. C1 FFN call, interleaved runs, previous routes against this one:
+ * M = 3 15.8 / 15.1-15.4 us (plan F2 18.3 / 18.6: not taken), 4 16.6 / 15.9, 6 18.8 / 16.7,
+ * 8 20.0 / 17.4, 12 22.5 / 19.1, 16 24.4 / 20.1; M = 2 ties. */
+static bool chunk_major_down(int M, int inter) {
+    const int G = inter / W4A16_GROUP;
+    return M >= 4 && M <= 16 && G >= 64 && G <= 192;
+}
+
 static int mlp_common(const uint16_t *normed, const uint8_t *gup, const uint16_t *gus,
                       const uint8_t *dnp, const uint16_t *dns, void *out, bool out_f32,
                       uint16_t *act, int M, int hidden, int inter, void *stream) {
@@ -1874,6 +1902,15 @@ static int mlp_common(const uint16_t *normed, const uint8_t *gup, const uint16_t
                              (size_t)M * hidden * (out_f32 ? 4 : 2));
     if (st < 0) return st;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (chunk_major_down(M, inter)) {
+        st = check_gemm_args(normed, gup, gus, act, M, 2 * inter, hidden, W4A16_GROUP,
+                             "mlp_int4 gate/up", (size_t)M * inter * 2);
+        if (st < 0) return st;
+        st = run_rows<kOutPairSilu>(normed, M, gup, gus, act, 2 * inter, hidden, s, 1);
+        if (st) return st;
+        return out_f32 ? launch_rows16x<true, true>(act, M, dnp, dns, out, hidden, inter, s)
+                       : launch_rows16x<false, true>(act, M, dnp, dns, out, hidden, inter, s);
+    }
     st = gate_up_silu_int4_bf16(normed, gup, gus, act, M, hidden, inter, stream);
     if (st) return st;
     return out_f32 ? run_rows<kOutF32>(act, M, dnp, dns, out, hidden, inter, s)
@@ -1974,11 +2011,15 @@ static int mlp_norm_common(const uint16_t *residual, const uint16_t *norm_w, int
                       * against 19.2 with the separate norm; M = 4 21.5 against 20.4-20.9 and
                       * M = 8 26.2-26.7 against 24.0, every block normalising all M rows) */
         st = launch_rows<true, false>(residual, M, gup, gus, act, 2 * inter, hidden, s, &na);
+    const bool cm = st > 0 && chunk_major_down(M, inter);
     if (st > 0) {
         st = launch_rmsnorm(normed, residual, norm_w, hidden, M, na.bias, eps, s);
-        if (!st) st = run_rows<kOutPairSilu>(normed, M, gup, gus, act, 2 * inter, hidden, s);
+        if (!st) st = run_rows<kOutPairSilu>(normed, M, gup, gus, act, 2 * inter, hidden, s, cm);
     }
     if (st) return st;
+    if (cm)
+        return out_f32 ? launch_rows16x<true, true>(act, M, dnp, dns, out, hidden, inter, s)
+                       : launch_rows16x<false, true>(act, M, dnp, dns, out, hidden, inter, s);
     return out_f32 ? run_rows<kOutF32>(act, M, dnp, dns, out, hidden, inter, s)
                    : run_rows<kOutBf16>(act, M, dnp, dns, out, hidden, inter, s);
 }
@@ -2054,9 +2095,11 @@ extern "C" int mlp_int4_residual_norm_bf16(uint16_t *residual, const uint16_t *s
         return set_error(W4A16_ERR_CONFIG, "mlp_int4_residual_norm: K=%d beyond the down kernels",
                          inter);
     }
+    const bool cm = chunk_major_down(M, inter);
     st = launch_rmsnorm(normed, residual, norm_w, hidden, M, na.bias, eps, s, sublayer);
-    if (!st) st = run_rows<kOutPairSilu>(normed, M, gup, gus, act, 2 * inter, hidden, s);
+    if (!st) st = run_rows<kOutPairSilu>(normed, M, gup, gus, act, 2 * inter, hidden, s, cm);
     if (st) return st;
+    if (cm) return launch_rows16x<false, true>(act, M, dnp, dns, out, hidden, inter, s, residual);
     if (M == 1 && dn_pairs > kMaxLoads) {
         /* the down kernel adds the output into the (already updated) residual itself */
         st = launch_xwave<false>(act, dnp, dns, out, hidden, inter, s, residual, nullptr);

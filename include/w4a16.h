@@ -129,8 +129,9 @@ int gate_up_silu_int4_bf16(const uint16_t *x, const uint8_t *gu_packed,
                            int intermediate, void *stream);
 
 /* The INT4 branch of the dense MLP (reference csrc/kernels/layers.cu:126-145): fused
- * gate/up/SiLU, then down. `act_ws` is caller workspace of M * intermediate BF16.
- * out [M, hidden] BF16. */
+ * gate/up/SiLU, then down. `act_ws` is caller workspace of M * intermediate BF16; it holds the
+ * intermediate in the order the down kernel reads: row-major [M, I], except chunk-major
+ * ([I / 8][M][8]) for 4 <= M <= 16 with I / 128 in 64..192. out [M, hidden] BF16. */
 int mlp_int4_bf16(const uint16_t *normed, const uint8_t *gu_packed, const uint16_t *gu_scales,
                   const uint8_t *dn_packed, const uint16_t *dn_scales, uint16_t *out,
                   uint16_t *act_ws, int M, int hidden, int intermediate, void *stream);
@@ -156,7 +157,7 @@ int w4a16_rmsnorm_bf16(uint16_t *out, const uint16_t *x, const uint16_t *weight,
  * residual [M, hidden], then the INT4 MLP. At M = 1 and M = 2 the norm is formed inside the
  * gate/up kernel's activation staging (no separate launch, no normed round trip; the normed
  * part of ws is then left unwritten); other M normalise into ws first. ws: M * (hidden +
- * intermediate) BF16 (normed, then act). The norm's scale is rounded once to FP32 from an FP64
+ * intermediate) BF16 (normed, then act in the order mlp_int4_bf16 gives it). The norm's scale is rounded once to FP32 from an FP64
  * sum of squares; the products are FlashInfer's FP32 ones in its order. */
 int mlp_int4_norm_bf16(const uint16_t *residual, const uint16_t *norm_w, int norm_style,
                        float eps, const uint8_t *gu_packed, const uint16_t *gu_scales,
