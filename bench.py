@@ -307,6 +307,10 @@ def main():
                    "ffn_frac_of_peak": round(ffn_gbs / HBM_PEAK_GBS, 4),
                    "wall_us_per_call": round(wall_us, 3),
                    "kernel_avg_us": {"dominant": round(k1_avg, 3), "second": round(k2_avg, 3)},
+                   # the down projection is timed through gemm_int4_bf16 on row-major rows;
+                   # from M = 4 the FFN call runs it on its chunk-major intermediate instead
+                   **({"second_as_timed": "gemm_int4_bf16 (row-major rows), not the FFN's "
+                       "chunk-major down kernel"} if 4 <= m <= 16 and not linear_only else {}),
                    "with_rmsnorm_us_per_call": None if norm_us is None else round(norm_us, 3),
                    "with_residual_rmsnorm_us_per_call": None if f2_us is None else round(f2_us, 3)},
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
