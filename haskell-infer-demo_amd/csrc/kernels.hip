@@ -775,9 +775,11 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
  * lanes l and l ^ 40 hold the two groups of a pair for the same (r, m).
  *
  * The activation goes from memory straight into LDS (buffer_load ... lds, 16 bytes a lane),
- * every load issued before the weight loads, in the order [pair][16-byte chunk c][row m][a]:
- * the 16 lanes of one ds_read_b128 pass (one k block, rows 8a + m) then read 16 consecutive
- * chunks, which covers every bank once. Chunks of a group past K are loaded as zeros.
+ * every load issued before the weight loads, in the order [pair][row m][a][16 chunks] with
+ * chunk c in slot c ^ (2 m + a): one load instruction reads four 256-byte runs (whole cache
+ * lines; the order [pair][chunk][row][a] read 64-byte half lines from M = 5), and the 16 lanes
+ * of one ds_read_b128 pass (one k block, rows 8a + m) hit 16 distinct 16-byte bank slots.
+ * Chunks of a group past K are loaded as zeros.
  * ---------------------------------------------------------------------------------------- */
 template <bool PAIR, bool OUT_F32, int TB, int SK, int NL, int MI, bool NORM = false>
 __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
@@ -809,14 +811,20 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
      * staged chunks 64 j .. 64 j + 63 */
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)M * cpr * 16);
     int xloads = 0;
+    /* staged chunk pos holds chunk c of row m of group 2 p + a, pos = ((p M + m) 2 + a) 16 +
+     * (c ^ (2 m + a)): one instruction reads four (row, group) runs of 256 contiguous bytes */
+    auto staged = [&](int pos, int &m, int &g, int &c) {
+        const int seg = pos >> 4, aa = seg & 1, t2 = seg >> 1;
+        m = t2 % M;
+        g = 2 * (t2 / M) + aa;
+        c = (pos & 15) ^ ((2 * m + aa) & 15);
+    };
     for (int j = wave; j < nins; j += W) {
         const int pos = j * 64 + lane;
-        const int t2 = pos >> 1;
-        const int m = t2 % M;
-        const int t3 = t2 / M;
-        const int g = 2 * (t3 >> 4) + (pos & 1);
+        int m, g, c;
+        staged(pos, m, g, c);
         const bool ok = pos < nlds && g < G;
-        const uint32_t off = ok ? (uint32_t)((m * cpr + g * 16 + (t3 & 15)) * 16) : kOob;
+        const uint32_t off = ok ? (uint32_t)((m * cpr + g * 16 + c) * 16) : kOob;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             xr, (__attribute__((address_space(3))) void *)(smem4 + j * 64), 16, off, 0, 0, 0);
         ++xloads;
@@ -867,9 +875,9 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
              * and rounded once to FP32: the correctly rounded scale whatever the summation
              * order, so this prologue and the FP64 restatement of the norm agree exactly */
             double ss = 0.0;
-            for (int j = lane; j < P * 32; j += 64) { /* row m's chunks: (pair, chunk, a) */
-                const int pp = j >> 5, c = (j >> 1) & 15, aa = j & 1;
-                const uint4 ch = smem4[(pp * 16 + c) * 2 * M + 2 * wave + aa];
+            for (int j = lane; j < P * 32; j += 64) { /* row m's chunks: (pair, a, slot) */
+                const int pp = j >> 5, aa = (j >> 4) & 1;
+                const uint4 ch = smem4[((pp * M + wave) * 2 + aa) * 16 + (j & 15)];
                 const uint32_t w4[4] = {ch.x, ch.y, ch.z, ch.w};
 #pragma unroll
                 for (int q2 = 0; q2 < 4; ++q2) {
@@ -885,9 +893,8 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
         }
         __syncthreads();
         for (int pos = tid; pos < nlds; pos += W * 64) {
-            const int t2 = pos >> 1;
-            const int m = t2 % M, t3 = t2 / M;
-            const int g = 2 * (t3 >> 4) + (pos & 1), c = t3 & 15;
+            int m, g, c;
+            staged(pos, m, g, c);
             if (g >= G) continue; /* a staged group past K is zero and stays zero */
             const float rm = rms[m];
             const uint4 v = smem4[pos];
@@ -911,7 +918,9 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
     /* 4. eight MFMAs a pair. A piece past the tile's groups has scale 0 (its loads read 0) and
      * its staged activation is zero, so it adds exactly 0 without a branch; lanes of A rows
      * m >= M read row M - 1 (their D rows are not used). */
-    const uint4 *abase = smem4 + (q * M + min(r, M - 1)) * 2 + a;
+    const int arow = min(r, M - 1);
+    const uint4 *abase = smem4 + (arow * 2 + a) * 16;
+    const int aswz = (2 * arow + a) & 15;
     const uint4 offs = make_uint4(0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u);
     f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -923,7 +932,7 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
             f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xa[t * 8 * M]);
+                const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xa[(4 * t + q) ^ aswz]);
                 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, unpack8(words[t]), d, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, offs),
                                                             d, 0, 0, 0);
