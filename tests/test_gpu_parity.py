@@ -298,6 +298,31 @@ def test_ffn_parity(cuda, hidden, inter, m):
     assert_parity(out, ref, f"ffn H={hidden} I={inter} M={m}", floor_div=16.0)
 
 
+@pytest.mark.parametrize("hidden,inter,m", [(256, 8192, 4), (256, 8064, 4), (256, 8192, 3),
+                                            (384, 24576, 16), (256, 24576, 5)])
+def test_ffn_chunk_major_bounds(cuda, hidden, inter, m):
+    """The FFN entry's chunk-major route at its edges: I / 128 = 64 (the least K it takes) and
+    192 (the most, 12 groups a wave, A loads kept 3 groups ahead), M = 4 (the least M), and
+    just outside (I / 128 = 63, M = 3: row-major through the public kernels). Each FFN output
+    against the oracle at the end-to-end bar, its workspace activation against the oracle's,
+    and the FP32 partial form against the oracle's unrounded partial."""
+    import torch
+
+    say(f"ffn chunk-major bounds H={hidden} I={inter} M={m}")
+    gup, gus, dp, ds = make_ffn(hidden, inter, layer=5)
+    x = oracle.synth_activation(m, hidden, seed=500 + m)
+    gu = w4a16.TiledWeight.from_artifact(gup, gus, 2 * inter, hidden, pair=True, device=cuda)
+    dn = w4a16.TiledWeight.from_artifact(dp, ds, hidden, inter, device=cuda)
+    xd = to_dev(x, cuda)
+    act_ws = torch.empty((m, inter), dtype=xd.dtype, device=cuda)
+    out = from_dev(w4a16.mlp_int4(xd, gu, dn, act_ws=act_ws))
+    ref, _, ref_act = oracle.ffn_bf16(x, gup, gus, dp, ds, hidden, inter)
+    assert_parity(ws_act(from_dev(act_ws), m, inter), ref_act, f"chunk-major act M={m} I={inter}")
+    assert_parity(out, ref, f"chunk-major FFN M={m} I={inter}", floor_div=16.0)
+    part = w4a16.mlp_int4(xd, gu, dn, act_ws=act_ws, partial_f32=True).cpu().numpy()
+    assert np.array_equal(oracle.bf16_bits(part), out)  # the partial rounds to the output
+
+
 def ws_act(flat, m, inter):
     """The intermediate as the FFN entry points leave it in their workspace: chunk-major
     ([I / 8 chunks][M rows][8 values]) from M = 4 to 16 when I / 128 is 64..192 (the
