@@ -184,6 +184,31 @@ def test_random_shapes_parity(cuda):
                           f"random gate/up M={m} I={inter} K={k}")
 
 
+def test_random_ffn_shapes_parity(cuda):
+    """Seeded random FFN shapes around the chunk-major route (M from 2 to 18, I / 128 from 60 to
+    100, hidden from 1 to 12 groups): mlp_int4 against the oracle FFN at the end-to-end bar,
+    and its workspace activation against the oracle's."""
+    import torch
+
+    rng = np.random.default_rng(2027)
+    for case in range(12):
+        m = int(rng.integers(2, 19))
+        hidden = 128 * int(rng.integers(1, 13))
+        inter = 128 * int(rng.integers(60, 101))
+        say(f"random ffn case {case}: M={m} H={hidden} I={inter}")
+        gup, gus, dp, ds = make_ffn(hidden, inter, layer=20 + case)
+        x = oracle.synth_activation(m, hidden, seed=3000 + case)
+        gu = w4a16.TiledWeight.from_artifact(gup, gus, 2 * inter, hidden, pair=True, device=cuda)
+        dn = w4a16.TiledWeight.from_artifact(dp, ds, hidden, inter, device=cuda)
+        xd = to_dev(x, cuda)
+        act_ws = torch.empty((m, inter), dtype=xd.dtype, device=cuda)
+        out = from_dev(w4a16.mlp_int4(xd, gu, dn, act_ws=act_ws))
+        ref, _, ref_act = oracle.ffn_bf16(x, gup, gus, dp, ds, hidden, inter)
+        assert_parity(ws_act(from_dev(act_ws), m, inter), ref_act,
+                      f"random ffn act M={m} H={hidden} I={inter}")
+        assert_parity(out, ref, f"random ffn M={m} H={hidden} I={inter}", floor_div=16.0)
+
+
 def test_long_k_routes(cuda):
     """K past the block-staged kernel: a pair operand at M = 1 (hidden 32768) runs the MFMA form
     with one live row; M = 4 at K = 65536 (the MFMA form, 64 K splits)."""
