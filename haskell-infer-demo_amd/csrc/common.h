@@ -36,6 +36,7 @@ namespace w4a16 {
 
 int set_error(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();
+const char *error_text(); /* the calling thread's last reason (what w4a16_last_error returns) */
 
 /* BF16 round-to-nearest-even of an FP32 bit pattern (the format's own rounding rule,
  * reference csrc/linear_weight.cpp:34-44). */

@@ -2,10 +2,11 @@
  * engine.cpp - The dense-FFN INT4 operand store behind engine_load_quantized_ffn, and the
  * decode-time FFN dispatch that reads it.
  *
- * An EngineHandle here carries what the loader needs from the reference engine's descriptor
- * (layer count, which layers are dense, hidden and intermediate sizes, the tensor-parallel
- * degree and this handle's rank, the device) and owns the device operands of every dense layer.
- * engine_load_quantized_ffn follows reference csrc/engine.cu:2207-2428:
+ * A W4A16Store carries what the loader needs from the reference engine's descriptor (layer
+ * count, which layers are dense, hidden and intermediate sizes, the tensor-parallel degree and
+ * this handle's rank, the device) and owns the device operands of every dense layer. The loader
+ * (w4a16_load_quantized_ffn, and engine_load_quantized_ffn for callers with no engine) follows
+ * reference csrc/engine.cu:2207-2428:
  *   - parse and validate weights.manifest.json;
  *   - refuse expert parallelism, a sidecar that does not cover every dense layer with an
  *     mlpGateUp pair and an mlpDown entry, and shapes that are not the checkpoint's;
@@ -17,7 +18,13 @@
  *     re-quantized).
  * Loading is all-or-nothing: on any refusal every buffer this call allocated is freed and the
  * handle keeps what it had. Every failure after argument checking returns W4A16_ERR_WEIGHTS
- * with the reason in engine_last_error(), as the reference's catch-all does (engine.cu:2423-2427).
+ * with the reason in the thread's last error, as the reference's catch-all does
+ * (engine.cu:2423-2427).
+ *
+ * Both exported loader names call one internal function, and nothing in the library calls an
+ * exported name: an engine that defines engine_load_quantized_ffn itself and calls
+ * w4a16_load_quantized_ffn from it never gets its own function called back (the library is also
+ * linked with -Bsymbolic-functions and exports only the names of include/w4a16.h).
  */
 #include <hip/hip_runtime.h>
 
@@ -70,12 +77,14 @@ struct LayerOperands {
 
 }  // namespace
 
-struct EngineHandle {
+struct W4A16Store {
     W4A16EngineConfig cfg;
+    int device = -1;     /* the device current at create; -1 if none was visible */
+    int int4_rows = 1;   /* tokens routed to INT4: 1, or int4_max_rows for verify rows */
     std::vector<unsigned char> dense;
     int local_inter = 0; /* intermediate columns this rank holds */
     std::vector<LayerOperands> layers;
-    DevBuf act_ws;       /* [max_tokens, hidden + local_inter] BF16 (normed, then act) */
+    DevBuf act_ws;       /* [int4_rows, hidden + local_inter] BF16 (normed, then act) */
     int quantized_layers = 0;
 };
 
@@ -125,7 +134,26 @@ int read_text(const std::string &path, std::string *out) {
     return W4A16_OK;
 }
 
-int load_impl(EngineHandle *eng, const std::string &root) {
+/* Makes the store's device current for the duration of an upload and restores the caller's. */
+struct DeviceScope {
+    int prev = -1;
+    bool changed = false, entered = false;
+    int enter(int dev) {
+        entered = true;
+        if (dev < 0) return set_error(W4A16_ERR_STATE, "the store was created with no device visible");
+        if (hipGetDevice(&prev) != hipSuccess) return set_error(W4A16_ERR_HIP, "hipGetDevice failed");
+        if (prev != dev) {
+            if (hipSetDevice(dev) != hipSuccess) return set_error(W4A16_ERR_HIP, "hipSetDevice(%d) failed", dev);
+            changed = true;
+        }
+        return W4A16_OK;
+    }
+    ~DeviceScope() {
+        if (changed) (void)hipSetDevice(prev);
+    }
+};
+
+int load_impl(W4A16Store *eng, const std::string &root) {
     const W4A16EngineConfig &c = eng->cfg;
     std::string json;
     int st = read_text(root + "/weights.manifest.json", &json);
@@ -147,6 +175,7 @@ int load_impl(EngineHandle *eng, const std::string &root) {
 
     const long long H = c.hidden, I = c.intermediate, r = c.tp_rank;
     const long long li = eng->local_inter;
+    DeviceScope on_device; /* entered before the first upload, after the host-side checks */
     std::vector<LayerOperands> staged(c.num_layers);
     for (int l = 0; l < c.num_layers; ++l) {
         if (!eng->dense[l]) continue;
@@ -179,13 +208,15 @@ int load_impl(EngineHandle *eng, const std::string &root) {
         slice_rows(sdp.data(), dp.data(), I / 2, 0, H, col_off / 2, li / 2);
         slice_rows(sds.data(), ds.data(), Gd * 2, 0, H, col_off / W4A16_GROUP * 2, lGd * 2);
         LayerOperands &op = staged[l];
+        if (!on_device.entered && (st = on_device.enter(eng->device))) return st;
         if ((st = upload_tiled(sgp, sgs, 2 * li, H, 1, &op.gu_packed, &op.gu_scales)) ||
             (st = upload_tiled(sdp, sds, H, li, 0, &op.dn_packed, &op.dn_scales)))
             return set_error(W4A16_ERR_WEIGHTS, "%s", join_error("upload: ").c_str());
         op.loaded = true;
     }
+    if (!on_device.entered && (st = on_device.enter(eng->device))) return st;
     DevBuf ws;
-    if (ws.alloc((size_t)c.max_tokens * (size_t)(H + li) * 2)) return W4A16_ERR_WEIGHTS;
+    if (ws.alloc((size_t)eng->int4_rows * (size_t)(H + li) * 2)) return W4A16_ERR_WEIGHTS;
     /* commit: only now does the handle see the new operands */
     eng->layers.swap(staged);
     eng->act_ws = std::move(ws);
@@ -195,9 +226,24 @@ int load_impl(EngineHandle *eng, const std::string &root) {
 
 }  // namespace
 
-extern "C" const char *engine_last_error(void) { return w4a16_last_error(); }
+/* The one loader body behind both exported names. */
+static int load_store(W4A16Store *eng, const char *manifest_dir, const char *what) {
+    if (!eng || !manifest_dir) return set_error(W4A16_ERR_CONFIG, "%s: null argument", what);
+    try {
+        const int st = load_impl(eng, manifest_dir);
+        if (st) {
+            const std::string why = error_text();
+            return set_error(W4A16_ERR_WEIGHTS, "%s: %s", what, why.c_str());
+        }
+        return W4A16_OK;
+    } catch (const std::exception &e) {
+        return set_error(W4A16_ERR_WEIGHTS, "%s: %s", what, e.what());
+    }
+}
 
-extern "C" EngineHandle *w4a16_engine_create(const W4A16EngineConfig *cfg) {
+extern "C" const char *engine_last_error(void) { return error_text(); }
+
+extern "C" W4A16Store *w4a16_engine_create(const W4A16EngineConfig *cfg) {
     if (!cfg) {
         set_error(W4A16_ERR_CONFIG, "engine_create: null config");
         return nullptr;
@@ -208,13 +254,23 @@ extern "C" EngineHandle *w4a16_engine_create(const W4A16EngineConfig *cfg) {
         set_error(W4A16_ERR_CONFIG, "engine_create: bad configuration");
         return nullptr;
     }
+    if (c.int4_max_rows < 0 || c.int4_max_rows > c.max_tokens) {
+        set_error(W4A16_ERR_CONFIG, "engine_create: int4_max_rows %d is outside 0..max_tokens (%d)",
+                  c.int4_max_rows, c.max_tokens);
+        return nullptr;
+    }
     if (c.intermediate % c.tp_size != 0) {
         set_error(W4A16_ERR_CONFIG, "engine_create: intermediate %d does not split over tp=%d",
                   c.intermediate, c.tp_size);
         return nullptr;
     }
-    auto eng = std::make_unique<EngineHandle>();
+    auto eng = std::make_unique<W4A16Store>();
     eng->cfg = c;
+    eng->cfg.layer_is_dense = nullptr; /* copied below; the caller's array need not outlive us */
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    eng->device = dev;
+    eng->int4_rows = c.int4_max_rows > 0 ? c.int4_max_rows : 1;
     eng->dense.assign((size_t)c.num_layers, 1);
     if (c.layer_is_dense)
         for (int l = 0; l < c.num_layers; ++l) eng->dense[l] = c.layer_is_dense[l] ? 1 : 0;
@@ -223,33 +279,52 @@ extern "C" EngineHandle *w4a16_engine_create(const W4A16EngineConfig *cfg) {
     return eng.release();
 }
 
-extern "C" void w4a16_engine_destroy(EngineHandle *eng) { delete eng; }
-
-extern "C" int engine_load_quantized_ffn(EngineHandle *eng, const char *manifest_dir) {
-    if (!eng || !manifest_dir) return set_error(W4A16_ERR_CONFIG, "engine_load_quantized_ffn: null argument");
-    try {
-        const int st = load_impl(eng, manifest_dir);
-        if (st) {
-            const std::string why = w4a16_last_error();
-            return set_error(W4A16_ERR_WEIGHTS, "engine_load_quantized_ffn: %s", why.c_str());
-        }
-        return W4A16_OK;
-    } catch (const std::exception &e) {
-        return set_error(W4A16_ERR_WEIGHTS, "engine_load_quantized_ffn: %s", e.what());
-    }
+extern "C" void w4a16_engine_destroy(W4A16Store *eng) {
+    if (!eng) return;
+    DeviceScope on_device; /* free the buffers on the device that holds them */
+    if (eng->device >= 0) (void)on_device.enter(eng->device);
+    delete eng;
 }
 
-extern "C" int w4a16_load_quantized_ffn(EngineHandle *eng, const char *manifest_dir) {
-    return engine_load_quantized_ffn(eng, manifest_dir);
+extern "C" int w4a16_load_quantized_ffn(W4A16Store *eng, const char *manifest_dir) {
+    return load_store(eng, manifest_dir, "w4a16_load_quantized_ffn");
 }
 
-extern "C" int engine_quantized_ffn_layers(const EngineHandle *eng) {
+extern "C" int engine_load_quantized_ffn(W4A16Store *eng, const char *manifest_dir) {
+    return load_store(eng, manifest_dir, "engine_load_quantized_ffn");
+}
+
+extern "C" int engine_quantized_ffn_layers(const W4A16Store *eng) {
     return eng ? eng->quantized_layers : 0;
 }
 
-extern "C" int engine_ffn_operands(const EngineHandle *eng, int layer, W4A16FfnOperands *out) {
+static bool layer_loaded(const W4A16Store *eng, int layer) {
+    return layer >= 0 && layer < eng->cfg.num_layers && eng->layers[layer].loaded;
+}
+
+extern "C" int engine_ffn_routes_int4(const W4A16Store *eng, int layer, int tokens, int verify_rows) {
+    if (!eng || !layer_loaded(eng, layer)) return 0;
+    return tokens == 1 || (verify_rows && tokens >= 1 && tokens <= eng->int4_rows);
+}
+
+/* What every forward checks before it launches: the row count against the INT4 routing limit
+ * (prefill rows stay on the engine's BF16 path), and that the store's device is current. */
+static int forward_checks(const W4A16Store *eng, int tokens, const char *what) {
+    if (!eng) return set_error(W4A16_ERR_CONFIG, "%s: null store", what);
+    if (tokens < 0 || tokens > eng->int4_rows)
+        return set_error(W4A16_ERR_CONFIG, "%s: %d tokens; this store routes at most %d rows to INT4 "
+                         "(int4_max_rows), larger batches stay on the BF16 weights", what, tokens,
+                         eng->int4_rows);
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev != eng->device)
+        return set_error(W4A16_ERR_STATE, "%s: the store's operands are on device %d, device %d is "
+                         "current", what, eng->device, dev);
+    return W4A16_OK;
+}
+
+extern "C" int engine_ffn_operands(const W4A16Store *eng, int layer, W4A16FfnOperands *out) {
     if (!eng || !out) return set_error(W4A16_ERR_CONFIG, "engine_ffn_operands: null argument");
-    if (layer < 0 || layer >= eng->cfg.num_layers || !eng->layers[layer].loaded)
+    if (!layer_loaded(eng, layer))
         return set_error(W4A16_ERR_STATE, "engine_ffn_operands: layer %d has no INT4 operands", layer);
     const LayerOperands &op = eng->layers[layer];
     out->gate_up_packed = static_cast<const uint8_t *>(op.gu_packed.ptr);
@@ -262,14 +337,12 @@ extern "C" int engine_ffn_operands(const EngineHandle *eng, int layer, W4A16FfnO
     return W4A16_OK;
 }
 
-static int ffn_forward(EngineHandle *eng, int layer, const uint16_t *normed, void *out,
+static int ffn_forward(W4A16Store *eng, int layer, const uint16_t *normed, void *out,
                        bool partial, int tokens, void *stream) {
-    W4A16FfnOperands op;
-    int st = engine_ffn_operands(eng, layer, &op);
+    int st = forward_checks(eng, tokens, "engine_ffn_forward");
     if (st) return st;
-    if (tokens < 0 || tokens > eng->cfg.max_tokens)
-        return set_error(W4A16_ERR_CONFIG, "engine_ffn_forward: %d tokens, this engine holds workspace for %d",
-                         tokens, eng->cfg.max_tokens);
+    W4A16FfnOperands op;
+    if ((st = engine_ffn_operands(eng, layer, &op))) return st;
     uint16_t *act = static_cast<uint16_t *>(eng->act_ws.ptr);
     return partial ? mlp_int4_partial_f32(normed, op.gate_up_packed, op.gate_up_scales, op.down_packed,
                                           op.down_scales, static_cast<float *>(out), act, tokens,
@@ -279,26 +352,24 @@ static int ffn_forward(EngineHandle *eng, int layer, const uint16_t *normed, voi
                                    op.hidden, op.intermediate, stream);
 }
 
-extern "C" int engine_ffn_forward(EngineHandle *eng, int layer, const uint16_t *normed,
+extern "C" int engine_ffn_forward(W4A16Store *eng, int layer, const uint16_t *normed,
                                   uint16_t *out, int tokens, void *stream) {
     return ffn_forward(eng, layer, normed, out, false, tokens, stream);
 }
 
-extern "C" int engine_ffn_forward_partial_f32(EngineHandle *eng, int layer,
+extern "C" int engine_ffn_forward_partial_f32(W4A16Store *eng, int layer,
                                               const uint16_t *normed, float *out, int tokens,
                                               void *stream) {
     return ffn_forward(eng, layer, normed, out, true, tokens, stream);
 }
 
-static int ffn_forward_norm(EngineHandle *eng, int layer, const uint16_t *residual,
+static int ffn_forward_norm(W4A16Store *eng, int layer, const uint16_t *residual,
                             const uint16_t *norm_w, int norm_style, float eps, void *out,
                             bool partial, int tokens, void *stream) {
-    W4A16FfnOperands op;
-    int st = engine_ffn_operands(eng, layer, &op);
+    int st = forward_checks(eng, tokens, "engine_ffn_forward_norm");
     if (st) return st;
-    if (tokens < 0 || tokens > eng->cfg.max_tokens)
-        return set_error(W4A16_ERR_CONFIG, "engine_ffn_forward_norm: %d tokens, this engine holds workspace for %d",
-                         tokens, eng->cfg.max_tokens);
+    W4A16FfnOperands op;
+    if ((st = engine_ffn_operands(eng, layer, &op))) return st;
     uint16_t *ws = static_cast<uint16_t *>(eng->act_ws.ptr);
     return partial ? mlp_int4_norm_partial_f32(residual, norm_w, norm_style, eps, op.gate_up_packed,
                                                op.gate_up_scales, op.down_packed, op.down_scales,
@@ -310,14 +381,14 @@ static int ffn_forward_norm(EngineHandle *eng, int layer, const uint16_t *residu
                                         op.intermediate, stream);
 }
 
-extern "C" int engine_ffn_forward_norm(EngineHandle *eng, int layer, const uint16_t *residual,
+extern "C" int engine_ffn_forward_norm(W4A16Store *eng, int layer, const uint16_t *residual,
                                        const uint16_t *norm_w, int norm_style, float eps,
                                        uint16_t *out, int tokens, void *stream) {
     return ffn_forward_norm(eng, layer, residual, norm_w, norm_style, eps, out, false, tokens,
                             stream);
 }
 
-extern "C" int engine_ffn_forward_norm_partial_f32(EngineHandle *eng, int layer,
+extern "C" int engine_ffn_forward_norm_partial_f32(W4A16Store *eng, int layer,
                                                    const uint16_t *residual,
                                                    const uint16_t *norm_w, int norm_style,
                                                    float eps, float *out, int tokens,
@@ -326,19 +397,17 @@ extern "C" int engine_ffn_forward_norm_partial_f32(EngineHandle *eng, int layer,
                             stream);
 }
 
-extern "C" int engine_ffn_forward_residual_norm(EngineHandle *eng, int layer, uint16_t *residual,
+extern "C" int engine_ffn_forward_residual_norm(W4A16Store *eng, int layer, uint16_t *residual,
                                                 const uint16_t *sublayer, const uint16_t *norm_w,
                                                 int norm_style, float eps, uint16_t *out,
                                                 int tokens, void *stream) {
-    W4A16FfnOperands op;
-    int st = engine_ffn_operands(eng, layer, &op);
+    int st = forward_checks(eng, tokens, "engine_ffn_forward_residual_norm");
     if (st) return st;
     if (eng->cfg.tp_size > 1)
         return set_error(W4A16_ERR_CONFIG, "engine_ffn_forward_residual_norm: tensor parallelism "
                          "adds the residual after the cross-rank sum; use engine_ffn_forward_norm_partial_f32");
-    if (tokens < 0 || tokens > eng->cfg.max_tokens)
-        return set_error(W4A16_ERR_CONFIG, "engine_ffn_forward_residual_norm: %d tokens, this engine holds workspace for %d",
-                         tokens, eng->cfg.max_tokens);
+    W4A16FfnOperands op;
+    if ((st = engine_ffn_operands(eng, layer, &op))) return st;
     return mlp_int4_residual_norm_bf16(residual, sublayer, norm_w, norm_style, eps,
                                        op.gate_up_packed, op.gate_up_scales, op.down_packed,
                                        op.down_scales, out, static_cast<uint16_t *>(eng->act_ws.ptr),

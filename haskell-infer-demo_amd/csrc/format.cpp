@@ -28,11 +28,13 @@ int set_error(int status, const char *fmt, ...) {
 
 void clear_error() { t_error[0] = '\0'; }
 
+const char *error_text() { return t_error; }
+
 }  // namespace w4a16
 
 using namespace w4a16;
 
-extern "C" const char *w4a16_last_error(void) { return t_error; }
+extern "C" const char *w4a16_last_error(void) { return error_text(); }
 
 /* ---------------------------------------------------------------------------------------- */
 /* BF16 and the shape rule                                                                   */

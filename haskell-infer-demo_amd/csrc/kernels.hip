@@ -405,6 +405,23 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
     }
 }
 
+/* The arrival step of a split-K combine, run by one wave of each of the `parts` blocks that
+ * share a counter, after its lanes have stored their partials (agent-scope atomic stores).
+ * Release: the wave's agent-scope release fence orders those stores before lane 0's counter
+ * increment (the wave's lanes issue in program order, so the fence covers every lane's stores).
+ * Acquire: the wave that takes the last arrival (returned value parts - 1) runs an agent-scope
+ * acquire fence before it reads any partial, so every block's stores, released before its
+ * increment, are visible to it (the increments form one release sequence on the counter).
+ * Returns the counter value before this wave's increment, on every lane. */
+__device__ __forceinline__ unsigned split_arrive(unsigned *counter, int parts, int lane) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    unsigned prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0);
+    if (prev == (unsigned)(parts - 1)) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    return prev;
+}
+
 /* GEMV with wave-local activation: as gemv_tiles_kernel, but each wave loads only the
  * activation of its own group pairs (512 bytes a pair, 8 bytes a lane, issued with its weight
  * loads) into a private LDS slice, and forms the per-(group, kb) sums with shuffles. No block
@@ -499,13 +516,7 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
     if (BS > 1) {
         float *pp = partial + (size_t)tile * BS * 8;
         __hip_atomic_store(pp + part * 8 + lane, row_sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);
-        unsigned prev = 0;
-        if (lane == 0)
-            prev = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-        prev = __shfl(prev, 0);
-        if (prev != BS - 1) return;
+        if (split_arrive(&counters[tile], BS, lane) != BS - 1) return;
         row_sum = 0.0f;
 #pragma unroll
         for (int j = 0; j < BS; ++j)
@@ -688,8 +699,8 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
 
     /* 5. split-K combine: publish, count, and let the last arrival sum in split order. The
      * partials and the counter are accessed with agent-scope atomics (coherent across the XCDs'
-     * L2 caches), and the wave waits for its partial stores to complete before it counts, so
-     * whoever reads count S - 1 sees every partial; no cache-wide fence is needed. */
+     * L2 caches); split_arrive puts a release before the count and an acquire after the last
+     * one, so whoever reads count S - 1 sees every partial. */
     if (S > 1) {
         float *mine = partial + ((size_t)ks * NT + tp) * 16 * M;
 #pragma unroll
@@ -697,13 +708,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
             if (4 * q + i < M)
                 __hip_atomic_store(mine + (4 * q + i) * 16 + n, acc[i], __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);
-        unsigned prev = 0;
-        if (lane == 0)
-            prev = __hip_atomic_fetch_add(&counters[tp], 1u, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-        prev = __shfl(prev, 0);
-        if (prev != (unsigned)(S - 1)) return;
+        if (split_arrive(&counters[tp], S, lane) != (unsigned)(S - 1)) return;
         /* the S partials are loaded in batches of 8 with every load issued before any is
          * summed (each is a round trip to the coherence point), then summed in split order */
 #pragma unroll

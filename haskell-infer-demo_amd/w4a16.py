@@ -83,6 +83,7 @@ _SIGNATURES = {
     "engine_last_error": (ctypes.c_char_p, []),
     "engine_quantized_ffn_layers": (_i, [_vp]),
     "engine_ffn_operands": (_i, [_vp, _i, _vp]),
+    "engine_ffn_routes_int4": (_i, [_vp, _i, _i, _i]),
     "engine_ffn_forward": (_i, [_vp, _i, _vp, _vp, _i, _vp]),
     "engine_ffn_forward_partial_f32": (_i, [_vp, _i, _vp, _vp, _i, _vp]),
     "engine_ffn_forward_norm": (_i, [_vp, _i, _vp, _vp, _i, ctypes.c_float, _vp, _i, _vp]),
@@ -480,7 +481,7 @@ def sha256_hex(data):
 class _EngineConfig(ctypes.Structure):
     _fields_ = [("num_layers", _i), ("layer_is_dense", ctypes.POINTER(ctypes.c_ubyte)),
                 ("hidden", _i), ("intermediate", _i), ("tp_size", _i), ("tp_rank", _i),
-                ("ep_size", _i), ("max_tokens", _i)]
+                ("ep_size", _i), ("max_tokens", _i), ("int4_max_rows", _i)]
 
 
 class FfnOperands(ctypes.Structure):
@@ -492,20 +493,22 @@ class Engine:
     """The INT4 FFN operand store of one GPU (EngineHandle)."""
 
     def __init__(self, num_layers, hidden, intermediate, tp_size=1, tp_rank=0, ep_size=1,
-                 max_tokens=16, dense=None):
+                 max_tokens=16, dense=None, int4_max_rows=0):
+        """int4_max_rows: verify rows routed to INT4 (0 = decode only, the reference's
+        ``tokens == 1`` predicate, csrc/kernels/layers.cu:126); forwards refuse more rows."""
         flags = None
         if dense is not None:
             self._dense = (ctypes.c_ubyte * num_layers)(*[1 if d else 0 for d in dense])
             flags = ctypes.cast(self._dense, ctypes.POINTER(ctypes.c_ubyte))
         cfg = _EngineConfig(num_layers, flags, hidden, intermediate, tp_size, tp_rank, ep_size,
-                            max_tokens)
+                            max_tokens, int4_max_rows)
         self.handle = lib.w4a16_engine_create(ctypes.byref(cfg))
         if not self.handle:
             raise W4A16Error(W4A16_ERR_CONFIG, f"engine_create: {last_error()}")
         self.hidden, self.intermediate, self.tp_size = hidden, intermediate, tp_size
 
     def close(self):
-        if self.handle:
+        if self.handle and lib is not None:  # lib is None only at interpreter shutdown
             lib.w4a16_engine_destroy(self.handle)
             self.handle = None
 
@@ -523,6 +526,10 @@ class Engine:
     @property
     def quantized_layers(self):
         return lib.engine_quantized_ffn_layers(self.handle)
+
+    def routes_int4(self, layer, tokens, verify_rows=False):
+        """engine_ffn_routes_int4: whether mlp_from_normed would take the INT4 branch."""
+        return bool(lib.engine_ffn_routes_int4(self.handle, layer, tokens, int(bool(verify_rows))))
 
     def operands(self, layer):
         op = FfnOperands()

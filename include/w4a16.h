@@ -211,8 +211,10 @@ int w4a16_sha256_hex(const void *data, size_t len, char *out_hex65);
 
 /* The store's handle. It carries the part of the reference engine that the INT4 path reads:
  * the descriptor's dense layers and FFN sizes, the tensor-parallel degree and this handle's
- * rank (one handle per GPU), and the device operands it loads. */
-typedef struct EngineHandle EngineHandle;
+ * rank (one handle per GPU), the device it was created on, and the device operands it loads.
+ * Its type name is the library's own: the reference engine's opaque EngineHandle is a
+ * different struct, and an engine that holds one store per device keeps both side by side. */
+typedef struct W4A16Store W4A16Store;
 
 typedef struct W4A16EngineConfig {
     int num_layers;
@@ -222,7 +224,8 @@ typedef struct W4A16EngineConfig {
     int tp_size;                         /* replicated tensor parallelism degree */
     int tp_rank;                         /* this handle's rank */
     int ep_size;                         /* expert parallelism (> 1 is refused at load) */
-    int max_tokens;                      /* largest M engine_ffn_forward accepts */
+    int max_tokens;                      /* workspace rows: the largest M a forward accepts */
+    int int4_max_rows;                   /* verify rows routed to INT4 (0 = 1, decode only) */
 } W4A16EngineConfig;
 
 /* Device operands of one layer, in tile order (the reference's LayerWeights::{gate_up_i4,
@@ -238,52 +241,71 @@ typedef struct W4A16FfnOperands {
 } W4A16FfnOperands;
 
 /* No reference counterpart: the reference engine_create (csrc/include/engine.h:69-72) builds
- * these fields from its descriptor. NULL on a bad configuration (w4a16_last_error()). */
-EngineHandle *w4a16_engine_create(const W4A16EngineConfig *cfg);
-void w4a16_engine_destroy(EngineHandle *engine);
+ * these fields from its descriptor. The store belongs to the device current at this call; the
+ * device entry points below refuse to run it from another. int4_max_rows must lie in
+ * 0..min(16, max_tokens). NULL on a bad configuration (w4a16_last_error()). */
+W4A16Store *w4a16_engine_create(const W4A16EngineConfig *cfg);
+void w4a16_engine_destroy(W4A16Store *store);
 
 /* Load the INT4 operands of every dense layer from manifest_dir (weights.manifest.json + the
  * artifacts it names): validated, SHA-256 checked, sliced to this rank with the global scales,
- * uploaded and re-laid on the device; all-or-nothing. W4A16_OK, W4A16_ERR_CONFIG for a null
- * argument, otherwise W4A16_ERR_WEIGHTS with the reason in engine_last_error().
- * Same signature and semantics as reference csrc/include/engine.h:98 (csrc/engine.cu:2207-2428). */
-int engine_load_quantized_ffn(EngineHandle *engine, const char *manifest_dir);
-/* The same function under a prefixed name, for an engine that defines the public name itself
- * and calls this loader per rank from inside it. */
-int w4a16_load_quantized_ffn(EngineHandle *engine, const char *manifest_dir);
+ * uploaded and re-laid on the store's device; all-or-nothing. W4A16_OK, W4A16_ERR_CONFIG for a
+ * null argument, otherwise W4A16_ERR_WEIGHTS with the reason in w4a16_last_error().
+ * The loader of reference csrc/engine.cu:2207-2428, for an engine that defines the public
+ * engine_load_quantized_ffn itself and calls this per rank from inside it. */
+int w4a16_load_quantized_ffn(W4A16Store *store, const char *manifest_dir);
 
-/* Reason of the calling thread's last failure (reference csrc/include/engine.h, engine_last_error). */
+/* Standalone aliases, for a caller with no engine of its own (a Haskell program or a ctypes
+ * harness linking only this library): the same loader under the reference's public name
+ * (reference csrc/include/engine.h:98, src/Infer/FFI/Engine.hs:114-115), its handle argument
+ * being this library's store, and the thread's last failure under the engine's name. Inside the
+ * library nothing calls either name: the library binds its own calls locally, so an engine
+ * whose definitions of these names come first in the load order (and call
+ * w4a16_load_quantized_ffn) cannot be re-entered by them. Translation units that also see the
+ * engine's engine.h define W4A16_NO_ENGINE_ALIASES before including this header. */
+#ifndef W4A16_NO_ENGINE_ALIASES
+int engine_load_quantized_ffn(W4A16Store *store, const char *manifest_dir);
 const char *engine_last_error(void);
+#endif
+
+/* The INT4 routing predicate of mlp_from_normed (reference csrc/kernels/layers.cu:126, there
+ * `tokens == 1 && gate_up_i4 && down_i4`): 1 if `layer` holds INT4 operands and either
+ * tokens == 1 (decode) or verify_rows is nonzero and tokens <= the store's int4_max_rows
+ * (speculative verification); 0 otherwise, so prefill (verify_rows = 0, tokens > 1) stays on
+ * the engine's BF16 weights and its logits stay bit-identical to a BF16-only engine's. */
+int engine_ffn_routes_int4(const W4A16Store *store, int layer, int tokens, int verify_rows);
 
 /* Number of dense layers holding INT4 operands (the reference's quantized_ffn_layers). */
-int engine_quantized_ffn_layers(const EngineHandle *engine);
+int engine_quantized_ffn_layers(const W4A16Store *store);
 
 /* The layer's device operands (W4A16_ERR_STATE if the layer has none). */
-int engine_ffn_operands(const EngineHandle *engine, int layer, W4A16FfnOperands *out);
+int engine_ffn_operands(const W4A16Store *store, int layer, W4A16FfnOperands *out);
 
 /* The INT4 branch of forward_mlp_prepared for one layer (reference csrc/kernels/layers.cu:126-145
  * and 163-169): normed [tokens, hidden] BF16 -> out [tokens, hidden] BF16 on `stream`, using the
- * handle's workspace. Under tensor parallelism the _partial_f32 form returns this rank's FP32
+ * handle's workspace. Every forward below refuses (W4A16_ERR_CONFIG, before any launch) tokens
+ * above max(1, int4_max_rows), and a call made while another device than the store's is current.
+ * Under tensor parallelism the _partial_f32 form returns this rank's FP32
  * down-projection partial, to be summed across ranks before rounding. */
-int engine_ffn_forward(EngineHandle *engine, int layer, const uint16_t *normed, uint16_t *out,
+int engine_ffn_forward(W4A16Store *store, int layer, const uint16_t *normed, uint16_t *out,
                        int tokens, void *stream);
-int engine_ffn_forward_partial_f32(EngineHandle *engine, int layer, const uint16_t *normed,
+int engine_ffn_forward_partial_f32(W4A16Store *store, int layer, const uint16_t *normed,
                                    float *out, int tokens, void *stream);
 
 /* forward_mlp (reference csrc/kernels/layers.cu:150-159) on a loaded layer: the post-attention
  * RMSNorm of residual [tokens, hidden] with the caller's norm weight (LayerWeights::post_norm_w,
  * kept by the engine with its BF16 weights; style and eps as ModelDims::norm_style / rms_eps),
  * then the INT4 MLP (see mlp_int4_norm_bf16). */
-int engine_ffn_forward_norm(EngineHandle *engine, int layer, const uint16_t *residual,
+int engine_ffn_forward_norm(W4A16Store *store, int layer, const uint16_t *residual,
                             const uint16_t *norm_w, int norm_style, float eps, uint16_t *out,
                             int tokens, void *stream);
-int engine_ffn_forward_norm_partial_f32(EngineHandle *engine, int layer, const uint16_t *residual,
+int engine_ffn_forward_norm_partial_f32(W4A16Store *store, int layer, const uint16_t *residual,
                                         const uint16_t *norm_w, int norm_style, float eps,
                                         float *out, int tokens, void *stream);
 
 /* Plan F2 on a loaded layer (see mlp_int4_residual_norm_bf16); refused under tensor parallelism,
  * where the residual add follows the cross-rank sum (reference csrc/layer_dispatch.cu:166-169). */
-int engine_ffn_forward_residual_norm(EngineHandle *engine, int layer, uint16_t *residual,
+int engine_ffn_forward_residual_norm(W4A16Store *store, int layer, uint16_t *residual,
                                      const uint16_t *sublayer, const uint16_t *norm_w,
                                      int norm_style, float eps, uint16_t *out, int tokens,
                                      void *stream);

@@ -142,15 +142,21 @@ def test_load_and_forward_tp2(cuda, model):
 
 
 def test_engine_rows_and_tp4(cuda, model):
-    """Verify rows through the engine (tokens = 4, 16: the MFMA form) at tp = 1, and rank 3 of
-    tp = 4 (slices of 2432 intermediate columns = 19 groups, reference csrc/engine.cu:2308-2395)
-    against the oracle on the same slice."""
+    """Verify rows through the engine (tokens = 4, 16: the MFMA form) at tp = 1, with the
+    routing switch on (int4_max_rows = 16), and rank 3 of tp = 4 (slices of 2432 intermediate
+    columns = 19 groups, reference csrc/engine.cu:2308-2395) against the oracle on the same
+    slice."""
     import torch
 
     out, arts = model
     gup, gus, dp, ds = arts[1]
-    eng = w4a16.Engine(LAYERS, H, I, max_tokens=16)
+    eng = w4a16.Engine(LAYERS, H, I, max_tokens=16, int4_max_rows=16)
     assert eng.load_quantized_ffn(out) == 0, eng.last_error()
+    # the routing predicate (reference csrc/kernels/layers.cu:126, extended to verify rows)
+    assert eng.routes_int4(1, 1) and eng.routes_int4(1, 1, verify_rows=True)
+    assert eng.routes_int4(1, 16, verify_rows=True) and not eng.routes_int4(1, 17, verify_rows=True)
+    assert not eng.routes_int4(1, 4)                  # prefill rows stay on BF16
+    assert not eng.routes_int4(LAYERS, 1)             # no such layer
     for tokens in (4, 16):
         print(f"engine tokens={tokens}", flush=True)
         x = oracle.synth_activation(tokens, H, 50 + tokens)
@@ -176,4 +182,33 @@ def test_engine_rows_and_tp4(cuda, model):
     want = oracle.ffn_partial_f32(x, sgp, sgs, sdp, sds, H, li)
     rel = np.linalg.norm(part.cpu().numpy().astype(np.float64) - want) / np.linalg.norm(want)
     assert rel <= 1e-3, rel
+    eng.close()
+
+
+def test_engine_decode_only_default(cuda, model):
+    """The default store (int4_max_rows = 0) routes exactly what the reference routes: one
+    decode token (reference csrc/kernels/layers.cu:126). Four rows are refused before any launch
+    and the output buffer is left untouched; four verify rows run once the switch is on
+    (reference tests/test_quantized_ffn.py:196-201: prefill must stay bitwise BF16)."""
+    import torch
+
+    out, arts = model
+    gup, gus, dp, ds = arts[1]
+    eng = w4a16.Engine(LAYERS, H, I, max_tokens=16)
+    assert eng.load_quantized_ffn(out) == 0, eng.last_error()
+    assert eng.routes_int4(1, 1) and not eng.routes_int4(1, 4, verify_rows=True)
+    x = torch.from_numpy(oracle.synth_activation(4, H, 54).view(np.int16)).to(cuda)
+    sentinel = torch.full((4, H), 0x1234, dtype=torch.int16, device=cuda)
+    with pytest.raises(w4a16.W4A16Error) as err:
+        eng.forward(1, x, out=sentinel)
+    assert err.value.status == w4a16.W4A16_ERR_CONFIG and "int4_max_rows" in str(err.value)
+    torch.cuda.synchronize()
+    assert bool((sentinel == 0x1234).all())
+    eng.close()
+    eng = w4a16.Engine(LAYERS, H, I, max_tokens=16, int4_max_rows=4)
+    assert eng.load_quantized_ffn(out) == 0, eng.last_error()
+    assert eng.routes_int4(1, 4, verify_rows=True) and not eng.routes_int4(1, 4)
+    got = eng.forward(1, x).cpu().numpy()
+    ref, _, _ = oracle.ffn_bf16(x.cpu().numpy().view(np.uint16), gup, gus, dp, ds, H, I)
+    assert_parity(got.view(np.uint16), ref, "engine verify rows=4", floor_div=16.0)
     eng.close()
