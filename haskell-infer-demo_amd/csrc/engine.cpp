@@ -181,6 +181,12 @@ int load_impl(W4A16Store *eng, const std::string &root) {
         if (!eng->dense[l]) continue;
         const PairEntry &pair = m.pairs[m.find_pair("mlpGateUp", l)];
         const Entry &down = m.entries[m.find_entry(l, "mlpDown")];
+        /* the loader slices gate rows then up rows, so the pair must say exactly that (the
+         * reference reader admits any two member roles that have entries) */
+        if (pair.member_role[0] != "mlpGate" || pair.member_role[1] != "mlpUp")
+            return set_error(W4A16_ERR_WEIGHTS, "layer %d's mlpGateUp pair lists members [%s, %s]; the loader "
+                             "needs [mlpGate, mlpUp] in that order", l, pair.member_role[0].c_str(),
+                             pair.member_role[1].c_str());
         if (pair.n != 2 * I || pair.k != H)
             return set_error(W4A16_ERR_WEIGHTS, "layer %d's mlpGateUp pair is [%lld, %lld], the checkpoint's gate+up is "
                              "[%lld, %lld]", l, pair.n, pair.k, 2 * I, H);

@@ -212,3 +212,32 @@ def test_engine_decode_only_default(cuda, model):
     ref, _, _ = oracle.ffn_bf16(x.cpu().numpy().view(np.uint16), gup, gus, dp, ds, H, I)
     assert_parity(got.view(np.uint16), ref, "engine verify rows=4", floor_div=16.0)
     eng.close()
+
+
+def test_engine_loads_converted_checkpoint(cuda, tmp_path):
+    """A BF16 safetensors checkpoint -> convert.convert_checkpoint -> engine_load_quantized_ffn ->
+    engine_ffn_forward on each dense layer, against the oracle FFN of the same source weights
+    (the loaded half of reference tests/test_quantization_converter.py's chain)."""
+    import torch
+
+    from test_converter import LAYER_FFNS, make_checkpoint
+    from test_converter import H as CH, I as CI
+
+    model, desc, weights = make_checkpoint(str(tmp_path))
+    out = str(tmp_path / "int4")
+    convert.convert_checkpoint(model, desc, out)
+    eng = w4a16.Engine(len(LAYER_FFNS), CH, CI, dense=[f == "dense" for f in LAYER_FFNS])
+    assert eng.load_quantized_ffn(out) == 0, eng.last_error()
+    assert eng.quantized_layers == 2
+    for layer in (0, 2):
+        print(f"converted checkpoint layer {layer}", flush=True)
+        gp, gs = oracle.quantize(weights[(layer, "gate")])
+        up, us = oracle.quantize(weights[(layer, "up")])
+        dp, ds = oracle.quantize(weights[(layer, "down")])
+        x = oracle.synth_activation(1, CH, 60 + layer)
+        got = eng.forward(layer, torch.from_numpy(x.view(np.int16)).to(cuda)).cpu().numpy()
+        ref, _, _ = oracle.ffn_bf16(x, np.concatenate([gp, up]), np.concatenate([gs, us]), dp, ds,
+                                    CH, CI)
+        assert_parity(got.view(np.uint16), ref, f"converted layer {layer}", floor_div=16.0)
+    assert not eng.routes_int4(1, 1)                    # the MoE layer keeps BF16
+    eng.close()
