@@ -37,6 +37,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <mutex>
@@ -1700,7 +1701,28 @@ struct SplitScratch {
 std::mutex g_scratch_mu;
 SplitScratch g_scratch[64];
 
+/* While an allocation-free entry point runs on this thread, the split-K kernels take their
+ * partials and counters from the static scratch array below instead of the growable buffer. */
+struct FixedScratch {
+    bool active = false;
+    float *partial = nullptr;
+    size_t partial_bytes = 0;
+    unsigned *counters = nullptr;
+    size_t ncounters = 0;
+};
+thread_local FixedScratch t_fixed;
+
 int split_scratch(size_t partial_bytes, size_t ncounters, float **partial, unsigned **counters) {
+    if (t_fixed.active) {
+        /* the entry point checked its shapes against these sizes before launching anything */
+        if (partial_bytes > t_fixed.partial_bytes || ncounters > t_fixed.ncounters)
+            return set_error(W4A16_ERR_CONFIG, "split-K needs %zu bytes and %zu counters, beyond the "
+                             "static scratch (%zu bytes, %zu counters)", partial_bytes, ncounters,
+                             t_fixed.partial_bytes, t_fixed.ncounters);
+        *partial = t_fixed.partial;
+        *counters = t_fixed.counters;
+        return W4A16_OK;
+    }
     int dev = 0;
     int st = hip_status(hipGetDevice(&dev), "hipGetDevice");
     if (st) return st;
@@ -1760,6 +1782,59 @@ MfmaPlan plan_mfma(int M, int N, int K) {
     p.partial_bytes = p.S > 1 ? (size_t)p.S * NT * 16 * M * 4 : 0;
     p.ncounters = p.S > 1 ? (size_t)NT : 0;
     return p;
+}
+
+/* ---- The allocation-free scratch ------------------------------------------------------------
+ * For callers that cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc): the split-K partials and arrival counters in one static
+ * device array, 256 KiB of counters then 16 MiB of FP32 partials, which each GPU holds for the
+ * life of the process. The host-side name `scratch` is only a stand-in for the device array, so
+ * host code uses the address hipGetSymbolAddress returns for the current device, never the name. */
+constexpr size_t kFixedCounters = 65536;
+constexpr size_t kFixedPartialBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kFixedCounters * 4 + kFixedPartialBytes];
+
+__global__ void zero_words_kernel(unsigned *p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+void *g_fixed_base[64]; /* per device: the address of `scratch` there (under g_scratch_mu) */
+
+/* The device's scratch address, looked up (and its counters cleared by a fill kernel on
+ * `stream`, which a graph capture may record) on the first call on that device. */
+int fixed_scratch(hipStream_t stream, unsigned char **base) {
+    int dev = 0;
+    int st = hip_status(hipGetDevice(&dev), "hipGetDevice");
+    if (st) return st;
+    if (dev < 0 || dev >= 64) return set_error(W4A16_ERR_CONFIG, "device ordinal %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_fixed_base[dev]) {
+        void *p = nullptr;
+        st = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (st) return st;
+        if (!p) return set_error(W4A16_ERR_HIP, "hipGetSymbolAddress(scratch) returned no address");
+        hipLaunchKernelGGL(zero_words_kernel, dim3((int)(kFixedCounters / 256)), dim3(256), 0, stream,
+                           static_cast<unsigned *>(p), (int)kFixedCounters);
+        st = hip_status(hipGetLastError(), "scratch counter clear");
+        if (st) return st;
+        g_fixed_base[dev] = p;
+    }
+    *base = static_cast<unsigned char *>(g_fixed_base[dev]);
+    return W4A16_OK;
+}
+
+/* An upper bound of the split-K scratch one [M, K] x [N, K]^T product of this library can ask
+ * for, whichever kernel it is routed to: the wave-local GEMV's tile split (at most 8 blocks a
+ * tile, M = 1) and the MFMA form's plan for a 16-row slice (smaller slices need less). */
+void split_bound(int M, int N, int K, size_t *partial_bytes, size_t *ncounters) {
+    const size_t tiles = (size_t)N / 8;
+    size_t pb = tiles * 8 * 8 * sizeof(float), nc = tiles;
+    const MfmaPlan p = plan_mfma(std::min(std::max(M, 1), 16), N, K);
+    pb = std::max(pb, p.partial_bytes);
+    nc = std::max(nc, p.ncounters);
+    *partial_bytes = pb;
+    *ncounters = nc;
 }
 
 template <int OUT, int XPRE>
@@ -1940,6 +2015,38 @@ extern "C" int mlp_int4_bf16(const uint16_t *normed, const uint8_t *gup, const u
                              const uint8_t *dnp, const uint16_t *dns, uint16_t *out,
                              uint16_t *act_ws, int M, int hidden, int inter, void *stream) {
     return mlp_common(normed, gup, gus, dnp, dns, out, false, act_ws, M, hidden, inter, stream);
+}
+
+extern "C" int mlp_int4_bf16_noalloc(const uint16_t *normed, const uint8_t *gup,
+                                     const uint16_t *gus, const uint8_t *dnp, const uint16_t *dns,
+                                     uint16_t *out, uint16_t *act_ws, int M, int hidden, int inter,
+                                     void *stream) {
+    if (M < 0 || hidden <= 0 || inter <= 0)
+        return set_error(W4A16_ERR_CONFIG, "mlp_int4_bf16_noalloc: bad extents M=%d hidden=%d inter=%d",
+                         M, hidden, inter);
+    if (M == 0) return W4A16_OK;
+    if ((long long)2 * inter > INT32_MAX)
+        return set_error(W4A16_ERR_CONFIG, "mlp_int4_bf16_noalloc: intermediate %d too large", inter);
+    size_t pb_gu, nc_gu, pb_dn, nc_dn;
+    split_bound(M, 2 * inter, hidden, &pb_gu, &nc_gu);
+    split_bound(M, hidden, inter, &pb_dn, &nc_dn);
+    const size_t pb = std::max(pb_gu, pb_dn), nc = std::max(nc_gu, nc_dn);
+    if (pb > kFixedPartialBytes || nc > kFixedCounters)
+        return set_error(W4A16_ERR_CONFIG, "mlp_int4_bf16_noalloc: M=%d hidden=%d inter=%d may need %zu "
+                         "bytes of split-K partials and %zu counters; the static scratch holds %zu "
+                         "and %zu", M, hidden, inter, pb, nc, kFixedPartialBytes, kFixedCounters);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    unsigned char *base = nullptr;
+    int st = fixed_scratch(s, &base);
+    if (st) return st;
+    t_fixed.partial = reinterpret_cast<float *>(base + kFixedCounters * 4);
+    t_fixed.partial_bytes = kFixedPartialBytes;
+    t_fixed.counters = reinterpret_cast<unsigned *>(base);
+    t_fixed.ncounters = kFixedCounters;
+    t_fixed.active = true;
+    st = mlp_common(normed, gup, gus, dnp, dns, out, false, act_ws, M, hidden, inter, stream);
+    t_fixed.active = false;
+    return st;
 }
 
 extern "C" int mlp_int4_partial_f32(const uint16_t *normed, const uint8_t *gup,

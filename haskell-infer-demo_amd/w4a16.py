@@ -62,6 +62,7 @@ _SIGNATURES = {
     "silu_mul_packed_bf16": (_i, [_vp, _vp, _i, _i, _vp]),
     "gate_up_silu_int4_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mlp_int4_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "mlp_int4_bf16_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "w4a16_rmsnorm_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, ctypes.c_float, _vp]),
     "mlp_int4_norm_bf16": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i,
                                 _i, _vp]),

@@ -26,7 +26,8 @@
  *   - Compute calls that overlap in time on one device must be ordered on one stream: the
  *     split-K kernels of the small-M path share one per-device scratch buffer. The first call
  *     of a shape may grow that buffer (an allocation and a device synchronisation), so make it
- *     before capturing calls into a HIP graph.
+ *     before capturing calls into a HIP graph, or use mlp_int4_bf16_noalloc, which never
+ *     allocates.
  */
 #ifndef W4A16_H
 #define W4A16_H
@@ -135,6 +136,21 @@ int gate_up_silu_int4_bf16(const uint16_t *x, const uint8_t *gu_packed,
 int mlp_int4_bf16(const uint16_t *normed, const uint8_t *gu_packed, const uint16_t *gu_scales,
                   const uint8_t *dn_packed, const uint16_t *dn_scales, uint16_t *out,
                   uint16_t *act_ws, int M, int hidden, int intermediate, void *stream);
+
+/* No counterpart in the reference: mlp_int4_bf16 for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, kernels and results; the split-K partials and counters live in a static device
+ * array of the library (256 KiB of counters and 16 MiB of partials a GPU, held until the
+ * process ends) instead of the growable per-device buffer, so no call allocates or
+ * synchronises. Shapes whose worst-case split-K need exceeds that array are refused with
+ * W4A16_ERR_CONFIG before anything is launched (every BASELINE shape up to M = 16 fits). The
+ * first call on a device looks the array up and clears its counters with a kernel on `stream`.
+ * Every call on one GPU shares the array: calls that overlap in time on one GPU race, so order
+ * them on one stream. */
+int mlp_int4_bf16_noalloc(const uint16_t *normed, const uint8_t *gu_packed,
+                          const uint16_t *gu_scales, const uint8_t *dn_packed,
+                          const uint16_t *dn_scales, uint16_t *out, uint16_t *act_ws, int M,
+                          int hidden, int intermediate, void *stream);
 
 /* Tensor-parallel slice: as mlp_int4_bf16, but the down projection's FP32 partial is written
  * unrounded (out_f32 [M, hidden]), to be summed across ranks before rounding. */
