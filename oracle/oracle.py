@@ -44,6 +44,8 @@ def _load():
         "orc_ffn_bf16": (ctypes.c_int, [_ll, _ll, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
         "orc_ffn_partial_f32": (ctypes.c_int, [_ll, _ll, _ll, _vp, _vp, _vp, _vp, _vp, _vp]),
         "orc_rmsnorm_bf16": (ctypes.c_int, [_ll, _ll, _vp, _vp, ctypes.c_int, ctypes.c_double, _vp]),
+        "orc_rmsnorm_f32order_bf16": (ctypes.c_int, [_ll, _ll, _vp, _vp, ctypes.c_int, ctypes.c_float,
+                                                     _vp, _vp]),
         "orc_residual_norm_bf16": (ctypes.c_int, [_ll, _ll, _vp, _vp, _vp, ctypes.c_int,
                                                   ctypes.c_double, _vp]),
         "orc_residual_add_bf16": (ctypes.c_int, [_ll, _vp, _vp]),
@@ -169,6 +171,18 @@ def rmsnorm_bf16(x_bits, w_bits, norm_style, eps):
     _ok(lib.orc_rmsnorm_bf16(rows, cols, _p(x), _p(_c(w_bits, np.uint16)), norm_style, eps,
                              _p(out)), "rmsnorm_bf16")
     return out
+
+
+def rmsnorm_f32order_bf16(x_bits, w_bits, norm_style, eps):
+    """The reference's in-tree FP32 order (residual_norm_kernel): returns (out bits [rows, cols],
+    per-row FP32 scales)."""
+    x = _c(x_bits, np.uint16)
+    rows, cols = (1, x.shape[0]) if x.ndim == 1 else x.shape
+    out = np.zeros((rows, cols), np.uint16)
+    rms = np.zeros(rows, np.float32)
+    _ok(lib.orc_rmsnorm_f32order_bf16(rows, cols, _p(x), _p(_c(w_bits, np.uint16)), norm_style,
+                                      eps, _p(out), _p(rms)), "rmsnorm_f32order_bf16")
+    return out, rms
 
 
 def residual_norm_bf16(residual_bits, sub_bits, w_bits, norm_style, eps):

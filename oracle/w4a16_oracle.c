@@ -296,3 +296,51 @@ int orc_residual_norm_bf16(long long rows, long long cols, uint16_t *residual,
     if (st) return st;
     return orc_rmsnorm_bf16(rows, cols, residual, w, norm_style, eps, out);
 }
+
+/* The reference's in-tree FP32 order (csrc/kernels/flashinfer_norm.cu:136-160, residual_norm_kernel
+ * launched with 256 threads a row, :169-171): thread t accumulates fmaf(v, v, .) over columns
+ * t, t + 256, ...; each 32-lane warp reduces with __shfl_down offsets 16, 8, 4, 2, 1 (lane 0's
+ * value is the pairwise tree (l, l + 16), (l, l + 8), ...); warp 0 then reduces the 8 warp totals
+ * (zeros in lanes 8..31) the same way; scale = rsqrt(total / cols + eps) in FP32, taken here as the
+ * correctly rounded 1 / sqrtf (the reference's rsqrtf is a hardware approximation whose bits are
+ * not specified); out = BF16((v * scale) * (bias + w)) in FP32. rms_out (optional) gets the
+ * per-row scale. */
+int orc_rmsnorm_f32order_bf16(long long rows, long long cols, const uint16_t *x, const uint16_t *w,
+                              int norm_style, float eps, uint16_t *out, float *rms_out) {
+    if (rows < 0 || cols <= 0 || !isfinite(eps) || eps <= 0.0f)
+        return fail(ORC_ERR_RANGE, "invalid shape or epsilon");
+    if (rows == 0) return ORC_OK;
+    if (!x || !w || !out) return fail(ORC_ERR_ARG, "null argument");
+    if (norm_style != 0 && norm_style != 1) return fail(ORC_ERR_ARG, "norm_style must be 0 or 1");
+    enum { kThreads = 256, kWarp = 32 };
+    for (long long r = 0; r < rows; ++r) {
+        const uint16_t *xr = x + r * cols;
+        float lane[kThreads];
+        for (int t = 0; t < kThreads; ++t) {
+            float s = 0.0f;
+            for (long long c = t; c < cols; c += kThreads) {
+                const float v = orc_bf16_to_f32(xr[c]);
+                s = fmaf(v, v, s);
+            }
+            lane[t] = s;
+        }
+        float totals[kWarp];
+        for (int wi = 0; wi < kWarp; ++wi) totals[wi] = 0.0f;
+        for (int wi = 0; wi < kThreads / kWarp; ++wi) {
+            float *l = lane + wi * kWarp;
+            for (int off = kWarp / 2; off > 0; off >>= 1)
+                for (int i = 0; i < off; ++i) l[i] = l[i] + l[i + off];
+            totals[wi] = l[0];
+        }
+        for (int off = kWarp / 2; off > 0; off >>= 1)
+            for (int i = 0; i < off; ++i) totals[i] = totals[i] + totals[i + off];
+        const float scale = 1.0f / sqrtf(totals[0] / (float)cols + eps);
+        if (rms_out) rms_out[r] = scale;
+        for (long long c = 0; c < cols; ++c) {
+            float wt = orc_bf16_to_f32(w[c]);
+            if (norm_style == 0) wt += 1.0f;
+            out[r * cols + c] = orc_f32_to_bf16(orc_bf16_to_f32(xr[c]) * scale * wt);
+        }
+    }
+    return ORC_OK;
+}

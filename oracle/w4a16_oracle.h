@@ -110,6 +110,14 @@ int orc_residual_norm_bf16(long long rows, long long cols, uint16_t *residual,
                            const uint16_t *sublayer, const uint16_t *w_bf16, int norm_style,
                            double eps, uint16_t *out_bf16);
 
+/* The RMSNorm in the reference's in-tree FP32 order (residual_norm_kernel, reference
+ * csrc/kernels/flashinfer_norm.cu:136-160): FP32 fmaf partial sums over 256 strided threads, the
+ * warp shuffle trees, then 1/sqrt in FP32 (correctly rounded, standing in for rsqrtf), then
+ * (v * scale) * (bias + w). rms_out (may be NULL) receives each row's FP32 scale. */
+int orc_rmsnorm_f32order_bf16(long long rows, long long cols, const uint16_t *x_bf16,
+                              const uint16_t *w_bf16, int norm_style, float eps,
+                              uint16_t *out_bf16, float *rms_out);
+
 /* dst[i] <- BF16(f32(dst[i]) + f32(src[i])) (reference csrc/kernels/gdn_norm.cu:121-129). */
 int orc_residual_add_bf16(long long n, uint16_t *dst, const uint16_t *src);
 

@@ -46,15 +46,21 @@ def parity_metrics(got_bits, ref, ref_is_bits=True, floor_div=64.0):
     mag = np.maximum(np.abs(r), rms / floor_div)
     ulp = np.exp2(np.floor(np.log2(np.maximum(mag, 1e-38))) - 7)
     ulps = diff / ulp
+    # the same difference in ULPs of each element's own value, without the floor: how many
+    # near-zero elements the floor admits beyond the north star's "<= 2 BF16 ULP"
+    own = diff / np.exp2(np.floor(np.log2(np.maximum(np.abs(r), 1e-38))) - 7)
     return {"rel_l2": rel_l2, "max_ulp": float(ulps.max()) if ulps.size else 0.0,
-            "n_over_1ulp": int((ulps > 1.0).sum()), "n": int(r.size)}
+            "n_over_1ulp": int((ulps > 1.0).sum()), "n": int(r.size),
+            "n_over_2ulp_own": int((own > 2.0).sum()),
+            "max_ulp_own": float(own.max()) if own.size else 0.0}
 
 
 def assert_parity(got_bits, ref, what, rel_l2=1e-3, max_ulp=2.0, ref_is_bits=True,
                   floor_div=64.0):
     m = parity_metrics(got_bits, ref, ref_is_bits, floor_div)
     print(f"{what}: rel_l2={m['rel_l2']:.3g} max_ulp={m['max_ulp']:.3g} "
-          f">1ulp={m['n_over_1ulp']}/{m['n']}", flush=True)
+          f">1ulp={m['n_over_1ulp']}/{m['n']} own>2ulp={m['n_over_2ulp_own']} "
+          f"(max own {m['max_ulp_own']:.3g})", flush=True)
     assert m["rel_l2"] <= rel_l2, (what, m)
     assert m["max_ulp"] <= max_ulp, (what, m)
     return m

@@ -387,6 +387,11 @@ def test_rmsnorm_parity(cuda, style):
         d = ulp_diff(got, want)
         assert d.max() <= 1, (rows, hidden, int(d.max()))
         assert np.mean(d == 0) >= 0.99
+        # the reference's in-tree FP32 order (flashinfer_norm.cu:136-160): within 1 BF16 ULP too
+        want32, _ = oracle.rmsnorm_f32order_bf16(x, w, style, 1e-6)
+        d32 = ulp_diff(got, want32)
+        say(f"  vs FP32-order restatement: max {int(d32.max())} ULP, {int((d32 > 0).sum())}/{d32.size} differ")
+        assert d32.max() <= 1, (rows, hidden, int(d32.max()))
 
 
 @pytest.mark.parametrize("style", [0, 1])

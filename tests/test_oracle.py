@@ -321,3 +321,73 @@ def test_residual_norm_and_add_closed_forms():
         r, n = oracle.residual_norm_bf16(x, x, w, style, 1e-20)
         assert np.array_equal(r, oracle.bf16_bits(2 * oracle.bf16_to_f32(x)))
         assert np.array_equal(n, oracle.rmsnorm_bf16(x, w, style, 1e-20))
+
+
+def test_rmsnorm_f32order_pinned():
+    """orc_rmsnorm_f32order_bf16, the reference's in-tree FP32 order (residual_norm_kernel,
+    reference csrc/kernels/flashinfer_norm.cu:136-160), against values that only that order
+    gives:
+
+    * 4096^2 = 2^24 in column 0 and 1 in columns 1 and 3: the warp tree adds lanes 1 and 3 first
+      (offset 2), so the total is exactly 2^24 + 2; a column-sequential FP32 sum gives 2^24
+      (2^24 + 1 rounds to even), so a sequential restatement fails here;
+    * the same with the ones in columns 33 and 35 (warp 1): the warp totals meet at offset 1,
+      again 2^24 + 2;
+    * the ones in columns 256 and 512 (thread 0's own stride): fmaf(1, 1, 2^24) rounds to 2^24
+      each time, total 2^24 (a tree over columns would give 2^24 + 2);
+    * the closed forms of the FP64 form hold here too (constant row -> bias + w, eps inside the
+      root, zero row -> zeros), and the two forms agree within one BF16 ULP on random rows.
+    """
+    cols = 768
+    w = oracle.bf16_bits(np.ones(cols, np.float32))
+    big = oracle.bf16_bits(np.float32([4096.0]))[0]
+    one = oracle.bf16_bits(np.float32([1.0]))[0]
+    for ones, total in (((1, 3), 2.0 ** 24 + 2), ((33, 35), 2.0 ** 24 + 2), ((256, 512), 2.0 ** 24)):
+        x = np.zeros(cols, np.uint16)
+        x[0] = big
+        x[list(ones)] = one
+        _, rms = oracle.rmsnorm_f32order_bf16(x, w, 1, 1e-6)
+        want = np.float32(1.0) / np.sqrt(np.float32(total) / np.float32(cols) + np.float32(1e-6))
+        assert rms[0] == want, (ones, rms[0], want)
+    rng = np.random.default_rng(6)
+    wr = oracle.bf16_bits(rng.normal(0.0, 0.25, 256).astype(np.float32))
+    wf = oracle.bf16_to_f32(wr).astype(np.float64)
+    for style, bias in ((0, 1.0), (1, 0.0)):
+        x = oracle.bf16_bits(np.full(256, 2.0, np.float32))
+        got, _ = oracle.rmsnorm_f32order_bf16(x, wr, style, 1e-20)
+        assert np.array_equal(got[0], oracle.bf16_bits((bias + wf).astype(np.float32)))
+        x = oracle.bf16_bits(np.ones(256, np.float32))
+        got, _ = oracle.rmsnorm_f32order_bf16(x, wr, style, 3.0)
+        assert np.array_equal(got[0], oracle.bf16_bits((0.5 * (bias + wf)).astype(np.float32)))
+        got, _ = oracle.rmsnorm_f32order_bf16(np.zeros(256, np.uint16), wr, style, 1e-6)
+        assert not np.any(got & 0x7FFF)
+
+
+def test_rmsnorm_order_impact():
+    """How far the FP64-scale form (what the kernels compute) is from the reference's FP32 order
+    on decode-like rows (BF16 ~N(0,1) times a power of two, hidden 2560 and 5120, both styles):
+    the per-row FP32 scales differ by at most 3 FP32 ULPs (the FP32 sum's rounding, then the
+    FP32 divide, root and reciprocal) and the normalised BF16 values by at most 1 BF16 ULP; the
+    share of values that differ is printed."""
+    rng = np.random.default_rng(8)
+    for hidden in (2560, 5120):
+        for style in (0, 1):
+            rows = 200
+            x = oracle.bf16_to_f32(oracle.synth_activation(rows, hidden, 70 + hidden + style))
+            x *= np.float32(2.0) ** rng.integers(-3, 4, size=(rows, 1)).astype(np.float32)
+            xb = oracle.bf16_bits(x)
+            wb = oracle.bf16_bits(rng.normal(0.0 if style == 0 else 1.0, 0.2, hidden).astype(np.float32))
+            f64 = oracle.rmsnorm_bf16(xb, wb, style, 1e-6)
+            f32, rms32 = oracle.rmsnorm_f32order_bf16(xb, wb, style, 1e-6)
+            ss = (oracle.bf16_to_f32(xb).astype(np.float64) ** 2).sum(axis=1)
+            rms64 = (1.0 / np.sqrt(ss / hidden + np.float32(1e-6))).astype(np.float32)
+            scale_ulps = np.abs(rms32.view(np.int32).astype(np.int64) - rms64.view(np.int32))
+            a = f64.astype(np.int64)
+            b = f32.astype(np.int64)
+            sa = np.where(a & 0x8000, -(a & 0x7FFF), a & 0x7FFF)
+            sb = np.where(b & 0x8000, -(b & 0x7FFF), b & 0x7FFF)
+            d = np.abs(sa - sb)
+            print(f"H={hidden} style={style}: rows with another scale {int((scale_ulps > 0).sum())}/"
+                  f"{rows}, values differing {int((d > 0).sum())}/{d.size}")
+            assert scale_ulps.max() <= 3
+            assert d.max() <= 1
