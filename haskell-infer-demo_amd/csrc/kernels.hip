@@ -406,21 +406,43 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
     }
 }
 
-/* The arrival step of a split-K combine, run by one wave of each of the `parts` blocks that
- * share a counter, after its lanes have stored their partials (agent-scope atomic stores).
- * Release: the wave's agent-scope release fence orders those stores before lane 0's counter
- * increment (the wave's lanes issue in program order, so the fence covers every lane's stores).
- * Acquire: the wave that takes the last arrival (returned value parts - 1) runs an agent-scope
- * acquire fence before it reads any partial, so every block's stores, released before its
- * increment, are visible to it (the increments form one release sequence on the counter).
- * Returns the counter value before this wave's increment, on every lane. */
-__device__ __forceinline__ unsigned split_arrive(unsigned *counter, int parts, int lane) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+/* Split-K combine without fences. Each block of a tile stores its FP32 partials into mailbox
+ * slots: one 64-bit atomic word holding the value in its low half and a written-flag of 1 in its
+ * high half, so a reader that sees the flag sees that value (one atomic object; no ordering
+ * between locations is needed). The block then counts its arrival on the tile's counter
+ * (relaxed). The one that takes the last arrival waits on each slot's flag (it is set: the
+ * writer stored it before counting, so it becomes visible; the wait is bounded all the same),
+ * sums the slots in split order (independent of arrival order) and clears every slot and the
+ * counter, so the next kernel, which the kernel boundary orders after these stores, finds them
+ * empty. Slots are cleared when the scratch is allocated. Agent-scope release/acquire fences
+ * would give the same guarantee through a write-back and an invalidation of the L2 caches, which
+ * multiplied the time of these kernels several times. */
+constexpr int kSlotWaitPolls = 1 << 16;
+
+__device__ __forceinline__ void slot_put(uint64_t *slot, float v) {
+    __hip_atomic_store(slot, (1ull << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t slot_peek(const uint64_t *slot) {
+    return __hip_atomic_load(const_cast<uint64_t *>(slot), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* The value of a slot whose first read was `w`, waiting for its flag if needed; clears it. */
+__device__ __forceinline__ float slot_take(uint64_t *slot, uint64_t w) {
+    for (int n = 0; (w >> 32) == 0 && n < kSlotWaitPolls; ++n) {
+        __builtin_amdgcn_s_sleep(1);
+        w = slot_peek(slot);
+    }
+    __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __uint_as_float((uint32_t)w);
+}
+
+/* Counts one block's arrival (lane 0) and returns the count before it on every lane. */
+__device__ __forceinline__ unsigned split_arrive(unsigned *counter, int lane) {
     unsigned prev = 0;
     if (lane == 0) prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __shfl(prev, 0);
-    if (prev == (unsigned)(parts - 1)) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    return prev;
+    return __shfl(prev, 0);
 }
 
 /* GEMV with wave-local activation: as gemv_tiles_kernel, but each wave loads only the
@@ -438,7 +460,7 @@ __device__ __forceinline__ unsigned split_arrive(unsigned *counter, int parts, i
 template <bool PAIR, bool OUT_F32, int SK, int NP, int BS>
 __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ wt,
-    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, float *partial,
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, uint64_t *partial,
     unsigned *counters, uint16_t *residual, const uint16_t *sub) {
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
@@ -515,13 +537,15 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
 
     /* 4. the BS blocks of the tile */
     if (BS > 1) {
-        float *pp = partial + (size_t)tile * BS * 8;
-        __hip_atomic_store(pp + part * 8 + lane, row_sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (split_arrive(&counters[tile], BS, lane) != BS - 1) return;
+        uint64_t *pp = partial + (size_t)tile * BS * 8;
+        slot_put(pp + part * 8 + lane, row_sum);
+        if (split_arrive(&counters[tile], lane) != BS - 1) return;
+        uint64_t w[BS];
+#pragma unroll
+        for (int j = 0; j < BS; ++j) w[j] = slot_peek(pp + j * 8 + lane);
         row_sum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < BS; ++j)
-            row_sum += __hip_atomic_load(pp + j * 8 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int j = 0; j < BS; ++j) row_sum += slot_take(pp + j * 8 + lane, w[j]);
         if (lane == 0)
             __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -591,7 +615,7 @@ template <int OUT, int XPRE, int MI>
 __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
     const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, int S, int GS,
-    float *__restrict__ partial, unsigned *__restrict__ counters, uint16_t *residual, int cm) {
+    uint64_t *__restrict__ partial, unsigned *__restrict__ counters, uint16_t *residual, int cm) {
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
     const int tiles = N >> 3;
@@ -698,37 +722,34 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
         }
     }
 
-    /* 5. split-K combine: publish, count, and let the last arrival sum in split order. The
-     * partials and the counter are accessed with agent-scope atomics (coherent across the XCDs'
-     * L2 caches); split_arrive puts a release before the count and an acquire after the last
-     * one, so whoever reads count S - 1 sees every partial. */
+    /* 5. split-K combine: publish, count, and let the last arrival sum in split order (mailbox
+     * slots, see slot_put). Only the rows < M are published and read. */
     if (S > 1) {
-        float *mine = partial + ((size_t)ks * NT + tp) * 16 * M;
+        uint64_t *mine = partial + ((size_t)ks * NT + tp) * 16 * M;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            if (4 * q + i < M)
-                __hip_atomic_store(mine + (4 * q + i) * 16 + n, acc[i], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        if (split_arrive(&counters[tp], S, lane) != (unsigned)(S - 1)) return;
-        /* the S partials are loaded in batches of 8 with every load issued before any is
-         * summed (each is a round trip to the coherence point), then summed in split order */
+            if (4 * q + i < M) slot_put(mine + (4 * q + i) * 16 + n, acc[i]);
+        if (split_arrive(&counters[tp], lane) != (unsigned)(S - 1)) return;
+        /* the S partials are read in batches of 8 with every load issued before any is summed
+         * (each is a round trip to the coherence point), then summed in split order */
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = 0.0f;
         for (int k0 = 0; k0 < S; k0 += 8) {
-            float v[8][MI];
+            uint64_t v[8][MI];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float *src = partial + ((size_t)min(k0 + j, S - 1) * NT + tp) * 16 * M;
+                uint64_t *src = partial + ((size_t)(k0 + j) * NT + tp) * 16 * M;
 #pragma unroll
                 for (int i = 0; i < MI; ++i)
-                    v[j][i] = __hip_atomic_load(src + min(4 * q + i, M - 1) * 16 + n,
-                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    v[j][i] = (k0 + j < S && 4 * q + i < M) ? slot_peek(src + (4 * q + i) * 16 + n) : 0ull;
             }
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
+            for (int j = 0; j < 8; ++j) {
+                uint64_t *src = partial + ((size_t)(k0 + j) * NT + tp) * 16 * M;
 #pragma unroll
                 for (int i = 0; i < MI; ++i)
-                    if (k0 + j < S) acc[i] += v[j][i];
+                    if (k0 + j < S && 4 * q + i < M) acc[i] += slot_take(src + (4 * q + i) * 16 + n, v[j][i]);
+            }
         }
         if (lane == 0)
             __hip_atomic_store(&counters[tp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1439,7 +1460,7 @@ int launch_gemv_cfg(const uint16_t *x, const uint8_t *w, const uint16_t *s, void
     return hip_status(hipGetLastError(), "gemv launch");
 }
 
-int split_scratch(size_t partial_bytes, size_t ncounters, float **partial, unsigned **counters);
+int split_scratch(size_t partial_bytes, size_t ncounters, uint64_t **partial, unsigned **counters);
 
 template <bool OUT_F32, int NP, int SK, int BS, bool PAIR = false>
 int launch_xwave_np(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N,
@@ -1448,10 +1469,10 @@ int launch_xwave_np(const uint16_t *x, const uint8_t *w, const uint16_t *s, void
     if (SK * BS * NP < (K / 128 + 1) / 2)
         return set_error(W4A16_ERR_CONFIG, "internal: a %d x %d x %d wave-local shape covers %d of %d "
                          "group pairs", BS, SK, NP, BS * SK * NP, (K / 128 + 1) / 2);
-    float *partial = nullptr;
+    uint64_t *partial = nullptr;
     unsigned *counters = nullptr;
     if (BS > 1) {
-        int st = split_scratch((size_t)(N / 8) * BS * 8 * sizeof(float), (size_t)(N / 8),
+        int st = split_scratch((size_t)(N / 8) * BS * 8 * sizeof(uint64_t), (size_t)(N / 8),
                                &partial, &counters);
         if (st) return st;
     }
@@ -1693,7 +1714,7 @@ int device_cus() {
  * one in total, since sizes double), so graphs captured before a growth stay valid. Calls that
  * overlap in time on one device share the scratch, so they must be ordered on one stream. */
 struct SplitScratch {
-    float *partial = nullptr;
+    uint64_t *partial = nullptr; /* mailbox slots (slot_put) */
     size_t partial_bytes = 0;
     unsigned *counters = nullptr;
     size_t ncounters = 0;
@@ -1705,14 +1726,14 @@ SplitScratch g_scratch[64];
  * partials and counters from the static scratch array below instead of the growable buffer. */
 struct FixedScratch {
     bool active = false;
-    float *partial = nullptr;
+    uint64_t *partial = nullptr; /* mailbox slots (slot_put) */
     size_t partial_bytes = 0;
     unsigned *counters = nullptr;
     size_t ncounters = 0;
 };
 thread_local FixedScratch t_fixed;
 
-int split_scratch(size_t partial_bytes, size_t ncounters, float **partial, unsigned **counters) {
+int split_scratch(size_t partial_bytes, size_t ncounters, uint64_t **partial, unsigned **counters) {
     if (t_fixed.active) {
         /* the entry point checked its shapes against these sizes before launching anything */
         if (partial_bytes > t_fixed.partial_bytes || ncounters > t_fixed.ncounters)
@@ -1738,6 +1759,10 @@ int split_scratch(size_t partial_bytes, size_t ncounters, float **partial, unsig
         sc.partial_bytes = 0;
         if (hipMalloc((void **)&sc.partial, want) != hipSuccess)
             return set_error(W4A16_ERR_ALLOC, "split-K scratch: hipMalloc(%zu) failed", want);
+        /* every slot starts empty (flag 0); kernels leave the slots they use empty */
+        st = hip_status(hipMemset(sc.partial, 0, want), "hipMemset split-K slots");
+        if (!st) st = hip_status(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        if (st) return st;
         sc.partial_bytes = want;
     }
     if (sc.ncounters < ncounters) {
@@ -1779,7 +1804,7 @@ MfmaPlan plan_mfma(int M, int N, int K) {
     p.xpre = pre <= 1 ? 1 : pre <= 2 ? 2 : pre <= 4 ? 4 : 8;
     p.grid = nblk * p.S;
     p.smem = (size_t)(chunks + p.GS * 16) * 16 + (size_t)M * p.GS * 4;
-    p.partial_bytes = p.S > 1 ? (size_t)p.S * NT * 16 * M * 4 : 0;
+    p.partial_bytes = p.S > 1 ? (size_t)p.S * NT * 16 * M * sizeof(uint64_t) : 0;
     p.ncounters = p.S > 1 ? (size_t)NT : 0;
     return p;
 }
@@ -1787,21 +1812,21 @@ MfmaPlan plan_mfma(int M, int N, int K) {
 /* ---- The allocation-free scratch ------------------------------------------------------------
  * For callers that cannot allocate device memory (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc): the split-K partials and arrival counters in one static
- * device array, 256 KiB of counters then 16 MiB of FP32 partials, which each GPU holds for the
- * life of the process. The host-side name `scratch` is only a stand-in for the device array, so
+ * device array, 256 KiB of counters then 32 MiB of partial slots (an FP32 value and a
+ * written-flag each, see slot_put), which each GPU holds for the life of the process. The host-side name `scratch` is only a stand-in for the device array, so
  * host code uses the address hipGetSymbolAddress returns for the current device, never the name. */
 constexpr size_t kFixedCounters = 65536;
-constexpr size_t kFixedPartialBytes = (size_t)16 << 20;
+constexpr size_t kFixedPartialBytes = (size_t)32 << 20;
 static __device__ __align__(256) unsigned char scratch[kFixedCounters * 4 + kFixedPartialBytes];
 
-__global__ void zero_words_kernel(unsigned *p, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0u;
+__global__ void zero_words_kernel(unsigned *p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
 }
 
 void *g_fixed_base[64]; /* per device: the address of `scratch` there (under g_scratch_mu) */
 
-/* The device's scratch address, looked up (and its counters cleared by a fill kernel on
+/* The device's scratch address, looked up (and the whole array cleared by a fill kernel on
  * `stream`, which a graph capture may record) on the first call on that device. */
 int fixed_scratch(hipStream_t stream, unsigned char **base) {
     int dev = 0;
@@ -1814,9 +1839,9 @@ int fixed_scratch(hipStream_t stream, unsigned char **base) {
         st = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
         if (st) return st;
         if (!p) return set_error(W4A16_ERR_HIP, "hipGetSymbolAddress(scratch) returned no address");
-        hipLaunchKernelGGL(zero_words_kernel, dim3((int)(kFixedCounters / 256)), dim3(256), 0, stream,
-                           static_cast<unsigned *>(p), (int)kFixedCounters);
-        st = hip_status(hipGetLastError(), "scratch counter clear");
+        hipLaunchKernelGGL(zero_words_kernel, dim3(2048), dim3(256), 0, stream,
+                           static_cast<unsigned *>(p), sizeof(scratch) / 4);
+        st = hip_status(hipGetLastError(), "scratch clear");
         if (st) return st;
         g_fixed_base[dev] = p;
     }
@@ -1829,7 +1854,7 @@ int fixed_scratch(hipStream_t stream, unsigned char **base) {
  * tile, M = 1) and the MFMA form's plan for a 16-row slice (smaller slices need less). */
 void split_bound(int M, int N, int K, size_t *partial_bytes, size_t *ncounters) {
     const size_t tiles = (size_t)N / 8;
-    size_t pb = tiles * 8 * 8 * sizeof(float), nc = tiles;
+    size_t pb = tiles * 8 * 8 * sizeof(uint64_t), nc = tiles;
     const MfmaPlan p = plan_mfma(std::min(std::max(M, 1), 16), N, K);
     pb = std::max(pb, p.partial_bytes);
     nc = std::max(nc, p.ncounters);
@@ -1839,7 +1864,7 @@ void split_bound(int M, int N, int K, size_t *partial_bytes, size_t *ncounters) 
 
 template <int OUT, int XPRE>
 int launch_mfma_x(const MfmaPlan &p, const uint16_t *x, int M, const uint8_t *w,
-                  const uint16_t *s, void *out, int N, int K, float *partial, unsigned *counters,
+                  const uint16_t *s, void *out, int N, int K, uint64_t *partial, unsigned *counters,
                   hipStream_t stream, uint16_t *residual, int cm) {
     if (M == 1)
         hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE, 1>), dim3(p.grid), dim3(kMfmaWaves * 64),
@@ -1861,7 +1886,7 @@ template <int OUT>
 int launch_mfma(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
                 int K, hipStream_t stream, uint16_t *residual = nullptr, int cm = 0) {
     const MfmaPlan p = plan_mfma(M, N, K);
-    float *partial = nullptr;
+    uint64_t *partial = nullptr;
     unsigned *counters = nullptr;
     if (p.S > 1) {
         int st = split_scratch(p.partial_bytes, p.ncounters, &partial, &counters);
@@ -2039,7 +2064,7 @@ extern "C" int mlp_int4_bf16_noalloc(const uint16_t *normed, const uint8_t *gup,
     unsigned char *base = nullptr;
     int st = fixed_scratch(s, &base);
     if (st) return st;
-    t_fixed.partial = reinterpret_cast<float *>(base + kFixedCounters * 4);
+    t_fixed.partial = reinterpret_cast<uint64_t *>(base + kFixedCounters * 4);
     t_fixed.partial_bytes = kFixedPartialBytes;
     t_fixed.counters = reinterpret_cast<unsigned *>(base);
     t_fixed.ncounters = kFixedCounters;

@@ -140,11 +140,11 @@ int mlp_int4_bf16(const uint16_t *normed, const uint8_t *gu_packed, const uint16
 /* No counterpart in the reference: mlp_int4_bf16 for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
  * arguments, kernels and results; the split-K partials and counters live in a static device
- * array of the library (256 KiB of counters and 16 MiB of partials a GPU, held until the
+ * array of the library (256 KiB of counters and 32 MiB of partial slots a GPU, held until the
  * process ends) instead of the growable per-device buffer, so no call allocates or
  * synchronises. Shapes whose worst-case split-K need exceeds that array are refused with
  * W4A16_ERR_CONFIG before anything is launched (every BASELINE shape up to M = 16 fits). The
- * first call on a device looks the array up and clears its counters with a kernel on `stream`.
+ * first call on a device looks the array up and clears the array with a kernel on `stream`.
  * Every call on one GPU shares the array: calls that overlap in time on one GPU race, so order
  * them on one stream. */
 int mlp_int4_bf16_noalloc(const uint16_t *normed, const uint8_t *gu_packed,

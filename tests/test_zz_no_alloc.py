@@ -91,7 +91,7 @@ def test_noalloc_graph_replay(cuda):
 
 
 def test_noalloc_refuses_oversized(cuda):
-    """A shape whose worst-case split-K partials exceed the 16 MiB array is refused before any
+    """A shape whose worst-case split-K partials exceed the 32 MiB array is refused before any
     launch (the output keeps its contents)."""
     import torch
 
