@@ -10,11 +10,15 @@ gate/up/SiLU kernel + down kernel) on the next set, inputs already resident in H
 
 ``--config 2`` runs the 27B FFN (hidden 5120, intermediate 17408) over 64 distinct layers
 (8.8 GB); ``--config 4`` its tp=2 rank-0 slice; ``--config 0`` the single K=2560, N=9728
-linear; ``--config 3`` config 1 at M = --m.
+linear; ``--config 3`` config 1 at M = --m; ``--config 5`` the single linear at the shape the
+reference publishes its one per-call INT4 figure for (N=4096, K=5120, M=1: 52.1 us, 207.6 GB/s
+on an A40, reference docs/plan-numeric-contract.md:1753), quoted beside this run's.
 
-Timing: the calls of one pass over the rotating sets are captured in a HIP graph and the graph
-is replayed; HIP events on the replay stream bracket the timed replays, so ``value`` is device
-time per call including the gaps between kernels, not Python's launch rate.
+Timing: the calls of one pass over the rotating sets are captured in a HIP graph (and the first
+steps % sets calls in a second graph); exactly --steps calls are replayed in the timed region,
+with a HIP event on the replay stream before it and after every pass, so ``value`` is device
+time per call over all --steps calls (gaps between kernels included, not Python's launch rate)
+and ``config.pass_us_per_call`` gives the median, min and max over the passes.
 
 Prints ONE JSON line. ``roofline`` is the dominant kernel's (the fused gate/up/SiLU GEMV):
 algorithmic bytes per launch (packed nibbles + BF16 scales of its weight) over its average
@@ -41,9 +45,9 @@ CACHE_ROTATE_BYTES = 512 << 20   # rotate at least this many weight bytes (MALL 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=512)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3, 4))
+    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3, 4, 5))
     ap.add_argument("--m", type=int, default=4, help="rows for --config 3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -63,6 +67,8 @@ def shapes(cfg, m):
         return 5120, 17408, 1, "config2: 27B dense FFN decode M=1 H=5120 I=17408, 64 layers"
     if cfg == 3:
         return 2560, 9728, m, f"config3: Qwen3-4B dense FFN verify rows M={m}"
+    if cfg == 5:
+        return 5120, 4096, 1, "config5: the reference's published shape, W4A16 linear M=1 K=5120 N=4096"
     return 5120, 8704, 1, "config4: tp=2 rank-0 slice of config2 (I/2=8704), FP32 partial"
 
 
@@ -93,7 +99,23 @@ def make_sets(torch, w4a16, hidden, inter, count, linear_only, seed=1234):
     return sets
 
 
+def _median_us(run, seconds, cap=50):
+    run()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        run()
+        times.append((time.perf_counter() - t0) * 1e6)
+        if len(times) >= cap:
+            break
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
 def cpu_baseline(sets, hidden, inter, m, linear_only, seconds):
+    """The reference's CPU path on the GPU box's host: (i) dequantize per call + FP32 BLAS matmul
+    (reported as value), (ii) the matmul alone on weights dequantized once (matmul_only)."""
     import numpy as np
 
     from oracle import oracle
@@ -109,30 +131,36 @@ def cpu_baseline(sets, hidden, inter, m, linear_only, seconds):
     if linear_only:
         p, s = (t.cpu().numpy() for t in keep)
         s = s.view(np.uint16)
+        xf = oracle.bf16_to_f32(x).reshape(m, hidden)
 
         def run():
             w = oracle.dequantize_numpy(p, s, inter, hidden)
-            return oracle.bf16_bits(oracle.bf16_to_f32(x).reshape(m, hidden) @ w.T)
+            return oracle.bf16_bits(xf @ w.T)
+
+        w_once = oracle.dequantize_numpy(p, s, inter, hidden)
+
+        def run_ii():
+            return oracle.bf16_bits(xf @ w_once.T)
     else:
         gp, gs, dp, ds = (t.cpu().numpy() for t in keep)
         gs, ds = gs.view(np.uint16), ds.view(np.uint16)
 
         def run():
             return oracle.ffn_cpu_baseline(x, gp, gs, dp, ds, hidden, inter)
-    run()
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        run()
-        times.append((time.perf_counter() - t0) * 1e6)
-        if len(times) >= 50:
-            break
-    times.sort()
-    return {"value": round(times[len(times) // 2], 1), "unit": "us per call", "cores": cores,
-            "kind": "port",
-            "sample": f"{len(times)} calls of numpy dequantize-per-call + FP32 BLAS matmul "
-                      f"(BF16 rounding at the reference's points) on one weight set, median"}
+
+        wgu = oracle.dequantize_numpy(gp, gs, 2 * inter, hidden)
+        wdn = oracle.dequantize_numpy(dp, ds, hidden, inter)
+
+        def run_ii():
+            return oracle.ffn_cpu_matmul_only(x, wgu, wdn, hidden, inter)
+    v_i, n_i = _median_us(run, seconds)
+    v_ii, n_ii = _median_us(run_ii, max(2.0, seconds / 3))
+    return {"value": round(v_i, 1), "unit": "us per call", "cores": cores, "kind": "port",
+            "sample": f"{n_i} calls of numpy dequantize-per-call + FP32 BLAS matmul (BF16 "
+                      f"rounding at the reference's points) on one weight set, median",
+            "matmul_only": {"value": round(v_ii, 1), "unit": "us per call",
+                            "sample": f"{n_ii} calls of the FP32 BLAS matmuls on weights "
+                                      f"dequantized once, median"}}
 
 
 def main():
@@ -148,7 +176,7 @@ def main():
     import w4a16
 
     hidden, inter, m, name = shapes(args.config, args.m)
-    linear_only = args.config == 0
+    linear_only = args.config in (0, 5)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     if linear_only:
@@ -186,35 +214,45 @@ def main():
         if not linear_only:
             w4a16.gemm_int4_bf16(act, sets[i % count][1], down_out)
 
-    # Launches are captured into HIP graphs (one graph = one pass over all rotating weight sets)
-    # so the timed region measures the device, not Python's launch rate.
-    def capture(fn):
-        for i in range(count):          # eager warm-up of exactly the captured work
+    # Launches are captured into HIP graphs (one graph = one pass over all rotating weight sets,
+    # plus one holding the first steps % count calls) so the timed region measures the device,
+    # not Python's launch rate.
+    def capture(fn, n=None):
+        n = count if n is None else n
+        for i in range(n):              # eager warm-up of exactly the captured work
             fn(i)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            for i in range(count):
+            for i in range(n):
                 fn(i)
         torch.cuda.synchronize()
         return graph
 
-    def timed(graph, steps, warmup):
-        reps = max(1, -(-steps // count))
+    def timed(fn, steps, warmup):
+        """Exactly `steps` calls of fn, replayed from graphs, after at least `warmup` untimed
+        calls; returns (device us per call over all steps, wall us per call, per-pass us per
+        call list)."""
+        full = capture(fn)
+        rest = steps % count
+        tail = capture(fn, rest) if rest else None
         for _ in range(max(1, -(-warmup // count))):
-            graph.replay()
+            full.replay()
         torch.cuda.synchronize()
         stream = torch.cuda.current_stream()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        passes = [(full, count)] * (steps // count) + ([(tail, rest)] if tail else [])
+        events = [torch.cuda.Event(enable_timing=True) for _ in range(len(passes) + 1)]
         t0 = time.perf_counter()
-        e0.record(stream)
-        for _ in range(reps):
+        events[0].record(stream)
+        for i, (graph, _) in enumerate(passes):
             graph.replay()
-        e1.record(stream)
+            events[i + 1].record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        calls = reps * count
-        return e0.elapsed_time(e1) * 1e3 / calls, wall * 1e6 / calls, calls
+        per_pass = [events[i].elapsed_time(events[i + 1]) * 1e3 / n
+                    for i, (_, n) in enumerate(passes)]
+        total_us = events[0].elapsed_time(events[-1]) * 1e3
+        return total_us / steps, wall * 1e6 / steps, per_pass
 
     if args.pmc_pass:
         for i in range(args.steps):
@@ -227,15 +265,14 @@ def main():
         print(json.dumps({"pmc_pass": name, "calls": args.steps, "copy_bytes": 256 << 20}))
         return
 
-    g_ffn = capture(ffn_call)
-    us_per_call, wall_us, calls = timed(g_ffn, args.steps, args.warmup)
-    ms_total = us_per_call * calls / 1e3
-    g_first = capture(first_kernel)
-    k1_avg, _, _ = timed(g_first, args.steps, args.warmup)
+    if args.steps < 1:
+        sys.exit("bench.py: --steps must be at least 1")
+    us_per_call, wall_us, per_pass = timed(ffn_call, args.steps, args.warmup)
+    ms_total = us_per_call * args.steps / 1e3
+    k1_avg, _, _ = timed(first_kernel, args.steps, args.warmup)
     k2_avg = 0.0
     if not linear_only:
-        g_second = capture(second_kernel)
-        k2_avg, _, _ = timed(g_second, args.steps, args.warmup)
+        k2_avg, _, _ = timed(second_kernel, args.steps, args.warmup)
     norm_us = f2_us = None
     if not linear_only:
         # forward_mlp: the same call with the post-attention RMSNorm folded in (plain style)
@@ -247,7 +284,7 @@ def main():
             gu, dn, _ = sets[i % count]
             w4a16.mlp_int4_norm(x, norm_w, 1, 1e-6, gu, dn, out=out, ws=ws, partial_f32=partial)
 
-        norm_us, _, _ = timed(capture(norm_call), args.steps, args.warmup)
+        norm_us, _, _ = timed(norm_call, args.steps, args.warmup)
         if not partial:
             # plan F2: residual update + norm + FFN + residual add (the residual drifts over the
             # replays, which changes no timing: the call's work does not depend on the values)
@@ -260,8 +297,7 @@ def main():
                 w4a16.mlp_int4_residual_norm(residual, sub, norm_w, 1, 1e-6, gu, dn, out=out,
                                              ws=ws)
 
-            f2_us, _, _ = timed(capture(f2_call), args.steps, args.warmup)
-    args.steps = calls
+            f2_us, _, _ = timed(f2_call, args.steps, args.warmup)
     # the kernel the library routes the dominant launch to (gate/up, or the linear of config 0)
     hidden_pairs = (hidden // 128 + 1) // 2
     m1_family = "gemv_xwave_kernel" if 6 < hidden_pairs <= 12 else "gemv_tiles_kernel"
@@ -276,6 +312,15 @@ def main():
     achieved = dom_bytes / (k1_avg * 1e-6) / 1e9
     traffic, traffic_src = None, None
     tag = f"config{args.config}" + (f"_m{m}" if args.config == 3 else "")
+    # the committed rocprofv3 kernel-trace average of the same kernel, as a cross-check of the
+    # live event timing (profiles/kernel_avg_<tag>.json, written from the --stats summary)
+    rocprof_avg, rocprof_src = None, None
+    kpath = os.path.join(ROOT, "profiles", f"kernel_avg_{tag}.json")
+    if os.path.exists(kpath):
+        with open(kpath) as handle:
+            kavg = json.load(handle)
+        rocprof_avg = kavg.get("dominant_avg_us")
+        rocprof_src = os.path.relpath(kpath, ROOT)
     tpath = os.path.join(ROOT, "profiles", f"traffic_{tag}.json")
     if os.path.exists(tpath):
         # HBM bytes per launch of this kernel from the committed rocprofv3 --pmc summary
@@ -290,6 +335,9 @@ def main():
             if kname.startswith(prefix):
                 traffic, traffic_src = entry["traffic_bytes"], os.path.relpath(tpath, ROOT)
     ffn_gbs = per_set / (us_per_call * 1e-6) / 1e9
+    srt = sorted(per_pass)
+    pass_stats = {"passes": len(per_pass), "median": round(srt[len(srt) // 2], 3),
+                  "min": round(srt[0], 3), "max": round(srt[-1], 3)}
 
     result = {
         "metric": "\u00b5s per INT4 FFN decode call (M=1) + achieved HBM GB/s vs peak, 1 MI355X",
@@ -306,6 +354,7 @@ def main():
                    "ffn_achieved_GBps": round(ffn_gbs, 1),
                    "ffn_frac_of_peak": round(ffn_gbs / HBM_PEAK_GBS, 4),
                    "wall_us_per_call": round(wall_us, 3),
+                   "pass_us_per_call": pass_stats,
                    "kernel_avg_us": {"dominant": round(k1_avg, 3), "second": round(k2_avg, 3)},
                    # the down projection is timed through gemm_int4_bf16 on row-major rows;
                    # from M = 4 the FFN call runs it on its chunk-major intermediate instead
@@ -316,8 +365,18 @@ def main():
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "traffic_source": traffic_src, "bytes_per_launch": dom_bytes},
+                     "traffic_source": traffic_src, "bytes_per_launch": dom_bytes,
+                     "avg_launch_us": round(k1_avg, 3), "rocprof_avg_us": rocprof_avg,
+                     "rocprof_source": rocprof_src,
+                     "frac_from_rocprof": None if not rocprof_avg else
+                     round(dom_bytes / (rocprof_avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
     }
+    if args.config == 5:
+        # the reference's own per-call figure at this shape, on its hardware (A40, ~696 GB/s)
+        result["config"]["reference_published"] = {
+            "us_per_call": 52.1, "GBps": 207.6, "hardware": "NVIDIA A40",
+            "frac_of_its_peak": round(207.6 / 696.0, 3),
+            "source": "reference docs/plan-numeric-contract.md:1753, docs/worklog.md:514"}
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(sets, hidden, inter, m, linear_only,
                                               args.cpu_seconds)

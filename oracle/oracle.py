@@ -237,6 +237,16 @@ def ffn_cpu_baseline(x_bits, gu_packed, gu_scales, dn_packed, dn_scales, hidden,
     return bf16_bits(act @ wdn.T)
 
 
+def ffn_cpu_matmul_only(x_bits, wgu, wdn, hidden, inter):
+    """CPU baseline variant (ii): the same FFN on weights dequantized once beforehand (FP32 [2I, H]
+    and [H, I]), so only the two matmuls and the SiLU run per call."""
+    x = bf16_to_f32(x_bits).reshape(-1, hidden)
+    mid = bf16_to_f32(bf16_bits(x @ wgu.T))
+    g, u = mid[:, :inter].astype(np.float64), mid[:, inter:].astype(np.float64)
+    act = bf16_to_f32(bf16_bits((g / (1.0 + np.exp(-g)) * u).astype(np.float32)))
+    return bf16_bits(act @ wdn.T)
+
+
 # ---- synthetic inputs ----------------------------------------------------------------------------
 
 def synth_weight(n, k, seed, std=0.02):
