@@ -145,6 +145,17 @@ __device__ __forceinline__ float piece_dot_dpp(uint4 piece, uint4 xq, float xsum
     return fmaf(32.0f, a, -24.0f * xsum);
 }
 
+/* The sum of the eight BF16 values of a 16-byte chunk as four chained packed dot products with
+ * (1, 1): exact products, FP32 sums, one VALU instruction per two values (unpacking each value
+ * to FP32 and adding costs three). */
+__device__ __forceinline__ float chunk_sum8(uint4 v) {
+    const bf16x2_t one = __builtin_bit_cast(bf16x2_t, 0x3F803F80u);
+    float s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, v.x), one, 0.0f, false);
+    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, v.y), one, s, false);
+    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, v.z), one, s, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, v.w), one, s, false);
+}
+
 /* SiLU with exp computed as 2^n * 2^(r * log2 e), -g = n ln2 + r, |r| <= ln2/2 (Cody-Waite
  * split of ln2 into a 16-bit head and a tail), 2^(.) by v_exp_f32 on the reduced argument and
  * the power of two by v_ldexp_f32. */
@@ -248,8 +259,8 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
     uint4 xv[kXIters];
 #pragma unroll
     for (int it = 0; it < kXIters; ++it) {
-        const int i = it * W * 64 + tid;
-        xv[it] = buf_load16(xr, i < xchunks ? (uint32_t)i * 16 : kOob);
+        /* chunks past K fall outside the descriptor's range and read zeros */
+        xv[it] = buf_load16(xr, (uint32_t)(it * W * 64 + tid) * 16);
     }
     uint4 nv[NORM ? kXIters : 1];
     uint4 sv[NORM ? kXIters : 1];
@@ -276,11 +287,11 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
     uint16_t sbits[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-        const int p = ks + i * SK;
-        const int g = 2 * p + half;
-        const bool ok = p < P && g < G;
-        buf[i] = buf_load16_stream(wr, ok ? (uint32_t)(g * 512 + piece * 16) : kOob);
-        sbits[i] = buf_load_u16(sr, ok ? (uint32_t)(g * 16 + r * 2) : kOob);
+        /* a group past the tile (g >= G, which covers p >= P) is past both descriptors' ranges
+         * and reads zeros, so no offset needs a condition */
+        const int g = 2 * (ks + i * SK) + half;
+        buf[i] = buf_load16_stream(wr, (uint32_t)(g * 512 + piece * 16));
+        sbits[i] = buf_load_u16(sr, (uint32_t)(g * 16 + r * 2));
     }
 
     /* 2b. NORM: the activation is the RMSNorm of x, formed here (every block sees all of x):
@@ -349,11 +360,7 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
     for (int it = 0; it < kXIters; ++it) {
         const int i = it * W * 64 + tid;
         if (i < xchunks) smem4[i] = xv[it];
-        const uint32_t w4[4] = {xv[it].x, xv[it].y, xv[it].z, xv[it].w};
-        float s8 = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            s8 += bf16_widen((uint16_t)(w4[q] & 0xFFFFu)) + bf16_widen((uint16_t)(w4[q] >> 16));
+        float s8 = chunk_sum8(xv[it]);
         /* chunk i = 16 g + 4 s + kb (16 consecutive chunks are one DPP row): add the four s
          * of one (g, kb), i.e. the lanes congruent mod 4 within the row, by two rotations */
         s8 += dpp_f32<kDppRowRor4>(s8);
@@ -487,22 +494,18 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
     const int xchunk = 16 * half + 4 * (lane & 3) + kb;
     uint4 xv[NP];
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const int p = gw + i * kStride;
-        xv[i] = buf_load16(xr, p < P ? (uint32_t)(p * 512 + xchunk * 16) : kOob);
-    }
+    for (int i = 0; i < NP; ++i) /* p >= P reads past K: zeros */
+        xv[i] = buf_load16(xr, (uint32_t)((gw + i * kStride) * 512 + xchunk * 16));
     const size_t tile_bytes = (size_t)G * 512;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wt + (size_t)tile * tile_bytes, (uint32_t)tile_bytes);
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(st + (size_t)tile * G * 8, (uint32_t)G * 16);
     uint4 buf[NP];
     uint16_t sbits[NP];
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const int p = gw + i * kStride;
-        const int g = 2 * p + half;
-        const bool ok = p < P && g < G;
-        buf[i] = buf_load16_stream(wr, ok ? (uint32_t)(g * 512 + piece * 16) : kOob);
-        sbits[i] = buf_load_u16(sr, ok ? (uint32_t)(g * 16 + r * 2) : kOob);
+    for (int i = 0; i < NP; ++i) { /* g >= G (and so p >= P) is past the tile: zeros */
+        const int g = 2 * (gw + i * kStride) + half;
+        buf[i] = buf_load16_stream(wr, (uint32_t)(g * 512 + piece * 16));
+        sbits[i] = buf_load_u16(sr, (uint32_t)(g * 16 + r * 2));
     }
 
     /* 2. per pair: the (half, kb) activation sum over the quad (two DPP adds), then the dot
@@ -511,14 +514,7 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
         if (gw + i * kStride < P) { /* wave-uniform: every lane of the wave takes part */
-            const uint32_t xw[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-            float h[2];
-#pragma unroll
-            for (int q = 0; q < 2; ++q)
-                h[q] = bf16_widen((uint16_t)(xw[2 * q] & 0xFFFFu)) + bf16_widen((uint16_t)(xw[2 * q] >> 16)) +
-                       bf16_widen((uint16_t)(xw[2 * q + 1] & 0xFFFFu)) +
-                       bf16_widen((uint16_t)(xw[2 * q + 1] >> 16));
-            float s8 = h[0] + h[1];
+            float s8 = chunk_sum8(xv[i]);
             s8 += dpp_f32<kDppQuadSwap1>(s8);
             const float xsum = s8 + dpp_f32<kDppQuadSwap2>(s8);
             acc = fmaf(piece_dot_dpp(buf[i], xv[i], xsum), bf16_widen(sbits[i]), acc);
@@ -665,11 +661,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
     float *xsum = reinterpret_cast<float *>(smem4 + chunks + cpr);
     auto stage = [&](int i, uint4 v) {
         if (i < chunks) smem4[i] = v;
-        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-        float s8 = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            s8 += bf16_widen((uint16_t)(w4[j] & 0xFFFFu)) + bf16_widen((uint16_t)(w4[j] >> 16));
+        float s8 = chunk_sum8(v);
         /* 16 consecutive chunks make one group of one row */
         s8 += dpp_f32<kDppQuadSwap1>(s8);
         s8 += dpp_f32<kDppQuadSwap2>(s8);
