@@ -298,42 +298,32 @@ def main():
                                              ws=ws)
 
             f2_us, _, _ = timed(f2_call, args.steps, args.warmup)
-    # the kernel the library routes the dominant launch to (gate/up, or the linear of config 0)
-    hidden_pairs = (hidden // 128 + 1) // 2
-    m1_family = "gemv_xwave_kernel" if 6 < hidden_pairs <= 12 else "gemv_tiles_kernel"
-    family = (m1_family if m == 1 else "gemv_rows_kernel" if m <= 8
-              else "gemv_rows16_kernel" if m <= 16 else "mfma_gemm_kernel")
+    # the dominant launch: the fused gate/up + SiLU kernel, or the linear of configs 0 and 5
     if linear_only:
         dom_bytes = per_set
-        dom_name = f"{family} (gemm_int4_bf16)"
+        dom_role = "gemm_int4_bf16"
     else:
         dom_bytes = 2 * inter * hidden // 2 + 2 * inter * hidden // 128 * 2
-        dom_name = f"{family} (fused gate/up + SiLU x up)"
+        dom_role = "fused gate/up + SiLU x up"
     achieved = dom_bytes / (k1_avg * 1e-6) / 1e9
-    traffic, traffic_src = None, None
     tag = f"config{args.config}" + (f"_m{m}" if args.config == 3 else "")
-    # the committed rocprofv3 kernel-trace average of the same kernel, as a cross-check of the
-    # live event timing (profiles/kernel_avg_<tag>.json, written from the --stats summary)
-    rocprof_avg, rocprof_src = None, None
+    # The committed rocprofv3 summaries of the same configuration (profiles/): the kernel the
+    # dominant launch runs and its kernel-trace average (a cross-check of the live event timing
+    # above), and its HBM bytes per launch from FETCH_SIZE / WRITE_SIZE scaled by a plain copy.
+    dom_kernel, rocprof_avg, rocprof_src, traffic, traffic_src = None, None, None, None, None
     kpath = os.path.join(ROOT, "profiles", f"kernel_avg_{tag}.json")
     if os.path.exists(kpath):
         with open(kpath) as handle:
-            kavg = json.load(handle)
-        rocprof_avg = kavg.get("dominant_avg_us")
+            dom = json.load(handle).get("dominant", {})
+        dom_kernel, rocprof_avg = dom.get("kernel"), dom.get("avg_us")
         rocprof_src = os.path.relpath(kpath, ROOT)
     tpath = os.path.join(ROOT, "profiles", f"traffic_{tag}.json")
     if os.path.exists(tpath):
-        # HBM bytes per launch of this kernel from the committed rocprofv3 --pmc summary
-        # (FETCH_SIZE and WRITE_SIZE scaled by a plain copy of known size).
         with open(tpath) as handle:
-            entries = json.load(handle).get(tag, {})
-        if family == "mfma_gemm_kernel":
-            prefix = "mfma_gemm_kernel<0" if linear_only else "mfma_gemm_kernel<1"
-        else:
-            prefix = f"{family}<false, false" if linear_only else f"{family}<true, false"
-        for kname, entry in entries.items():
-            if kname.startswith(prefix):
-                traffic, traffic_src = entry["traffic_bytes"], os.path.relpath(tpath, ROOT)
+            dom = json.load(handle).get("dominant", {})
+        traffic = dom.get("traffic_bytes")
+        traffic_src = os.path.relpath(tpath, ROOT) if traffic else None
+    dom_name = f"{dom_kernel or 'gemv'} ({dom_role})"
     ffn_gbs = per_set / (us_per_call * 1e-6) / 1e9
     srt = sorted(per_pass)
     pass_stats = {"passes": len(per_pass), "median": round(srt[len(srt) // 2], 3),
