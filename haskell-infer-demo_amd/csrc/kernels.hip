@@ -211,6 +211,15 @@ __device__ __forceinline__ uint16_t buf_load_u16(__amdgpu_buffer_rsrc_t r, uint3
 
 constexpr uint32_t kOob = 0x80000000u; /* an offset no buffer here reaches: reads return 0 */
 
+/* u / d for 0 <= u < 69905 and 1 <= d <= 16 as (u * ceil(2^20 / d)) >> 20: exact in that range
+ * (the rounding excess of the multiplier, at most 15 / 2^20 per unit of u, stays below 1 / d),
+ * and with d wave-uniform the multiplier is one scalar computation, where an integer division
+ * costs a few dozen VALU instructions per use. div_magic(d) gives the multiplier. */
+__device__ __forceinline__ uint32_t div_magic(int d) { return ((1u << 20) + (uint32_t)d - 1u) / (uint32_t)d; }
+__device__ __forceinline__ int div_small(int u, uint32_t magic) {
+    return (int)(((uint32_t)u * magic) >> 20);
+}
+
 /* s_waitcnt immediate that waits until at most N vector memory operations are outstanding
  * (vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at their maxima, i.e. not waited on):
  * with the NL weight and NL scale loads of a wave issued last, N = 2 NL waits for everything
@@ -631,12 +640,13 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
     /* 1. the activation chunks of this block's K range (8 BF16 each; row m, chunk c) */
     const int cpr = ng * 16;            /* chunks per activation row */
     const int chunks = M * cpr;
+    const uint32_t ndiv = div_magic(ng); /* row of chunk i: (i / 16) / ng, ng <= 8 */
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)M * K * 2);
     uint4 xv[XPRE];
 #pragma unroll
     for (int it = 0; it < XPRE; ++it) {
         const int i = it * kMfmaWaves * 64 + tid;
-        const int m = i / cpr, c = i - m * cpr;
+        const int m = div_small(i >> 4, ndiv), c = i - m * cpr;
         xv[it] = buf_load16(xr, i < chunks ? (uint32_t)((m * K + g0 * 128 + c * 8) * 2) : kOob);
     }
 
@@ -673,7 +683,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
     for (int it = 0; it < XPRE; ++it) stage(it * kMfmaWaves * 64 + tid, xv[it]);
     for (int i0 = XPRE * kMfmaWaves * 64; i0 < chunks; i0 += kMfmaWaves * 64) {
         const int i = i0 + tid;
-        const int m = i / cpr, c = i - m * cpr;
+        const int m = div_small(i >> 4, ndiv), c = i - m * cpr;
         stage(i, buf_load16(xr, i < chunks ? (uint32_t)((m * K + g0 * 128 + c * 8) * 2) : kOob));
     }
     __syncthreads();
@@ -832,10 +842,12 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
     int xloads = 0;
     /* staged chunk pos holds chunk c of row m of group 2 p + a, pos = ((p M + m) 2 + a) 16 +
      * (c ^ (2 m + a)): one instruction reads four (row, group) runs of 256 contiguous bytes */
+    const uint32_t mdiv = div_magic(M); /* t2 < P * M <= 640 */
     auto staged = [&](int pos, int &m, int &g, int &c) {
         const int seg = pos >> 4, aa = seg & 1, t2 = seg >> 1;
-        m = t2 % M;
-        g = 2 * (t2 / M) + aa;
+        const int pq = div_small(t2, mdiv);
+        m = t2 - pq * M;
+        g = 2 * pq + aa;
         c = (pos & 15) ^ ((2 * m + aa) & 15);
     };
     for (int j = wave; j < nins; j += W) {
@@ -1032,12 +1044,12 @@ __global__ __launch_bounds__(1024) void gemv_rows16_kernel(
 
     /* 1. the activation, straight into LDS */
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)M * cpr * 16);
+    const uint32_t mdiv = div_magic(M); /* pos / 16 < G * M <= 640 within the LDS limit */
     for (int j = wave; j < nins; j += W) {
         const int pos = j * 64 + lane;
-        const int g = pos / (16 * M);
-        const int rem = pos - g * 16 * M;
-        const int m = rem >> 4;
-        const int c = (rem & 15) ^ (m & 15);
+        const int g = div_small(pos >> 4, mdiv);
+        const int m = (pos >> 4) - g * M;
+        const int c = (pos & 15) ^ (m & 15);
         const uint32_t off = pos < nlds ? (uint32_t)((m * cpr + g * 16 + c) * 16) : kOob;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             xr, (__attribute__((address_space(3))) void *)(smem4 + j * 64), 16, off, 0, 0, 0);
