@@ -111,7 +111,10 @@ def test_quantize_device_bit_exact(cuda):
                                  # including odd group counts
                                  (64, 1792), (64, 2816), (40, 3072), (16, 2944), (56, 1920),
                                  # 33 to 36 pairs: twelve waves of three pairs a tile
-                                 (512, 8448 + 128), (128, 8704), (64, 9216)])
+                                 (512, 8448 + 128), (128, 8704), (64, 9216),
+                                 # 17 to 20 pairs: ten waves of two pairs a tile (the
+                                 # reference's published shape first; 35 groups is odd)
+                                 (4096, 5120), (64, 4352), (48, 4480)])
 def test_gemv_parity(cuda, n, k):
     say(f"gemv n={n} k={k}")
     p, s = make_weight(n, k, seed=n + k)
