@@ -6,9 +6,11 @@
  * G = K/128, so one tile's groups are contiguous. Inside a unit, 32 pieces of 16 bytes: piece
  * p = kb * 8 + r holds row r of the tile and, in its dword s (0..3), the eight codes
  * k = g*128 + 32*s + 8*kb + j, j = 0..7. Inside that dword the code for j = 2q sits at bits
- * [4q, 4q+3] and the code for j = 2q+1 at bits [16+4q, 16+4q+3], so one shift and one mask put
- * the pair (k, k+1) into the two halves of a register, which is the operand shape of the
- * packed BF16 dot product and of the MFMA B operand. A wave's 64 lanes, each loading one
+ * [3+4q, 6+4q] and the code for j = 2q+1 at bits [19+4q, 22+4q], modulo 32 (the dword is rotated
+ * left by 3 bits, so the code j = 7 occupies bits 31 and 0-2), so a mask, after no shift for
+ * q = 0, a shift for q = 1, 2 and a rotation for q = 3, puts the pair (k, k+1) at bits 3-6 of the
+ * two halves of a register, which is the operand shape of the packed BF16 dot product and of
+ * the MFMA B operand. A wave's 64 lanes, each loading one
  * 16-byte piece, read 1 KiB contiguous (two units of one tile).
  *
  * The BF16 scales follow the same unit order: scale (t, g, r) at index (t * G + g) * 8 + r.
@@ -78,17 +80,18 @@ W4A16_HD long long tile_dword_index(long long t, long long g, long long groups, 
 }
 
 /* Artifact word (nibble j of eight consecutive codes at bits 4j) -> tile word (even j at
- * 4*(j/2), odd j at 16 + 4*(j/2)), and back. */
+ * 3 + 4*(j/2), odd j at 19 + 4*(j/2), modulo 32), and back. */
 W4A16_HD uint32_t spread_nibbles(uint32_t w) {
     uint32_t out = 0;
     for (int q = 0; q < 4; ++q) {
         out |= ((w >> (8 * q)) & 0xFu) << (4 * q);
         out |= ((w >> (8 * q + 4)) & 0xFu) << (16 + 4 * q);
     }
-    return out;
+    return (out << 3) | (out >> 29);
 }
 
 W4A16_HD uint32_t gather_nibbles(uint32_t t) {
+    t = (t >> 3) | (t << 29);
     uint32_t out = 0;
     for (int q = 0; q < 4; ++q) {
         out |= ((t >> (4 * q)) & 0xFu) << (8 * q);

@@ -3,7 +3,7 @@
  *
  * Weights are read in the tile order described in common.h. The M = 1 kernels are wave64
  * GEMVs: each lane loads one 16-byte piece (32 codes of one row) per step with a single
- * buffer_load_dwordx4, turns each pair of codes into a BF16 pair with a shift and one
+ * buffer_load_dwordx4, turns each pair of codes into a BF16 pair with at most one shift and one
  * v_bitop3_b32 (value 0.5 + u/32, u = nibble ^ 8 = code + 8, exact in BF16), and accumulates with
  * the packed BF16 dot product v_dot2c_f32_bf16 against the activation pair, whose activation
  * operand is broadcast over DPP from the lane of its quad that holds it. Since code = 32 v - 24,
@@ -90,19 +90,34 @@ __device__ __forceinline__ float lane_sum32(float v) {
     return x + y;
 }
 
-/* Code pairs as BF16. In a tile word the pair (j = 2q, 2q+1) sits at bits 4q and 16 + 4q, so one
- * shift puts both nibbles at bits 3-6 of their 16-bit halves and one v_bitop3_b32 computes
- * (s & 0x00780078) ^ 0x3F403F40: it keeps the two nibbles, flips their sign bits (u = code + 8)
- * and sets the exponent byte 0x3F (the mask and the constant are disjoint but for the sign bits).
- * The BF16 value is 2^-1 * (1 + u/16) = 0.5 + u/32 = 0.75 + code/32, exact. Keeping the nibble in
- * the top mantissa bits keeps the offset small (0.75 against a code step of 1/32), so the FP32
- * sums lose little to the offset that is subtracted afterwards. */
+/* Code pairs as BF16. In a tile word the pair (j = 2q, 2q+1) sits at bits 3 + 4q and 19 + 4q
+ * (the word is stored rotated left by 3 bits, so the odd code of q = 3 wraps round to bits 31 and
+ * 0-2): pair 0 already sits at bits 3-6 of its two 16-bit halves, pairs 1 and 2 get there by a
+ * right shift of 4q and pair 3 by a rotation of 12 (v_alignbit_b32), and one v_bitop3_b32 then
+ * computes (s & 0x00780078) ^ 0x3F403F40: it keeps the two nibbles, flips their sign bits
+ * (u = code + 8) and sets the exponent byte 0x3F (the mask and the constant are disjoint but for
+ * the sign bits). Three shifts and four bit operations a word, where a pair order that needs a
+ * shift for every pair costs four and four. The BF16 value is 2^-1 * (1 + u/16) = 0.5 + u/32 =
+ * 0.75 + code/32, exact. Keeping the nibble in the top mantissa bits keeps the offset small
+ * (0.75 against a code step of 1/32), so the FP32 sums lose little to the offset that is
+ * subtracted afterwards. */
 __device__ __forceinline__ uint32_t code_pair(uint32_t shifted) {
     return (shifted & 0x00780078u) ^ 0x3F403F40u;
 }
 
-/* sum_{j<32} code_j * x_j for one 16-byte piece (row r, k block kb of a group): 32 * dot(v, x) -
- * 24 * xsum, with v = 0.75 + code/32 from the unpack above and xsum the sum of the 32 x values.
+/* The four BF16 code pairs of a tile word, in k order. */
+__device__ __forceinline__ uint4 code_pairs(uint32_t word) {
+    uint4 v;
+    v.x = code_pair(word);
+    v.y = code_pair(word >> 4);
+    v.z = code_pair(word >> 8);
+    v.w = code_pair(__builtin_amdgcn_alignbit(word, word, 12));
+    return v;
+}
+
+/* (1/32) sum_{j<32} code_j * x_j for one 16-byte piece (row r, k block kb of a group):
+ * dot(v, x) - 0.75 xsum (one rounding), with v = 0.75 + code/32 from the unpack above and xsum the
+ * sum of the 32 x values; callers multiply their accumulated sum by 32 (exact) once.
  * The activation comes from the lane's quad through DPP: quad lane s holds the 8 values
  * 32 s + 8 kb + (0..7) of the group as four dwords, and every v_dot2c reads its activation
  * operand from quad lane s by a quad_perm broadcast, so no lane needs more than its own 16 bytes
@@ -118,10 +133,11 @@ __device__ __forceinline__ float piece_dot_dpp(uint4 piece, uint4 xq, float xsum
     uint32_t c[16];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        c[4 * s] = code_pair(w[s] << 3);
-        c[4 * s + 1] = code_pair(w[s] >> 1);
-        c[4 * s + 2] = code_pair(w[s] >> 5);
-        c[4 * s + 3] = code_pair(w[s] >> 9);
+        const uint4 v = code_pairs(w[s]);
+        c[4 * s] = v.x;
+        c[4 * s + 1] = v.y;
+        c[4 * s + 2] = v.z;
+        c[4 * s + 3] = v.w;
     }
     float a = 0.0f;
 #define W4A16_DOT2_DPP(S, X, C)                                                                  \
@@ -142,7 +158,7 @@ __device__ __forceinline__ float piece_dot_dpp(uint4 piece, uint4 xq, float xsum
                    "v"(c[3]), "v"(c[4]), "v"(c[5]), "v"(c[6]), "v"(c[7]), "v"(c[8]), "v"(c[9]),
                    "v"(c[10]), "v"(c[11]), "v"(c[12]), "v"(c[13]), "v"(c[14]), "v"(c[15]));
 #undef W4A16_DOT2_DPP
-    return fmaf(32.0f, a, -24.0f * xsum);
+    return fmaf(-0.75f, xsum, a);
 }
 
 /* The sum of the eight BF16 values of a 16-byte chunk as four chained packed dot products with
@@ -391,6 +407,7 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
             acc = fmaf(piece_dot_dpp(buf[i], xq, xsum[4 * g + kb]), bf16_widen(sbits[i]), acc);
         }
     }
+    acc *= 32.0f; /* piece_dot_dpp returns its sum over 32 */
 
     /* 5. lanes r, r+8, ..., r+56 hold row r's partials; then the SK waves of a tile */
     acc += dpp_f32<kDppRowRor8>(acc);
@@ -529,6 +546,7 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
             acc = fmaf(piece_dot_dpp(buf[i], xv[i], xsum), bf16_widen(sbits[i]), acc);
         }
     }
+    acc *= 32.0f; /* piece_dot_dpp returns its sum over 32 */
 
     /* 3. lanes r, r+8, ..., r+56 hold row r's partials; then the SK waves of the block */
     acc += dpp_f32<kDppRowRor8>(acc);
@@ -608,12 +626,7 @@ constexpr int kMfmaWaves = 4;   /* tile pairs per block */
 enum { kOutBf16 = 0, kOutPairSilu = 1, kOutF32 = 2 };
 
 __device__ __forceinline__ bf16x8_t unpack8(uint32_t word) {
-    uint4 v;
-    v.x = code_pair(word << 3);
-    v.y = code_pair(word >> 1);
-    v.z = code_pair(word >> 5);
-    v.w = code_pair(word >> 9);
-    return __builtin_bit_cast(bf16x8_t, v);
+    return __builtin_bit_cast(bf16x8_t, code_pairs(word));
 }
 
 template <int OUT, int XPRE, int MI>

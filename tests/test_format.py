@@ -91,6 +91,7 @@ def tile_numpy(packed, scales, n, k, pair):
     x = x.transpose(0, 2, 4, 1, 3, 5)                                   # t g kb r s j
     pos = np.array([4 * (j // 2) + 16 * (j % 2) for j in range(8)], np.uint32)
     dwords = (x << pos).sum(axis=-1, dtype=np.uint64).astype(np.uint32)
+    dwords = (dwords << np.uint32(3)) | (dwords >> np.uint32(29))      # stored rotated left by 3
     sc = np.asarray(scales, np.uint16).reshape(n, groups)[rows.reshape(-1)]
     sc = sc.reshape(tiles, 8, groups).transpose(0, 2, 1)
     return dwords.reshape(-1).view(np.uint8), sc.reshape(-1)
