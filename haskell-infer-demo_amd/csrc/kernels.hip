@@ -65,10 +65,13 @@ constexpr int kDppRowRor4 = 0x124;       /* row_ror:4 */
 constexpr int kDppRowRor8 = 0x128;       /* row_ror:8: lane ^ 8 within a row */
 constexpr int kDppRowShl4 = 0x104;       /* row_shl:4: lane l reads lane l + 4 of its row */
 
+/* The value of v in the lane the DPP pattern names (a lane with no source reads 0: the bound
+ * control that lets the compiler fold the move into the VALU instruction that uses it, e.g. one
+ * v_add_f32_dpp instead of a v_mov_b32_dpp and a v_add_f32). */
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
     return __builtin_bit_cast(
-        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
 /* v + v[l ^ 16] and v + v[l ^ 32] over the wave, on every lane, by the gfx950 lane swaps
@@ -116,8 +119,9 @@ __device__ __forceinline__ uint4 code_pairs(uint32_t word) {
 }
 
 /* (1/32) sum_{j<32} code_j * x_j for one 16-byte piece (row r, k block kb of a group):
- * dot(v, x) - 0.75 xsum (one rounding), with v = 0.75 + code/32 from the unpack above and xsum the
- * sum of the 32 x values; callers multiply their accumulated sum by 32 (exact) once.
+ * dot(v, x) - 0.75 xsum, with v = 0.75 + code/32 from the unpack above and xsum the sum of the 32
+ * x values; the chain starts from a0 = -0.75 xsum (quad_offset) and callers multiply their
+ * accumulated sum by 32 (exact) once.
  * The activation comes from the lane's quad through DPP: quad lane s holds the 8 values
  * 32 s + 8 kb + (0..7) of the group as four dwords, and every v_dot2c reads its activation
  * operand from quad lane s by a quad_perm broadcast, so no lane needs more than its own 16 bytes
@@ -128,7 +132,7 @@ __device__ __forceinline__ uint4 code_pairs(uint32_t word) {
  * needs a wait state before a following VALU instruction reads it (the trailing s_nop 1; without
  * it the last product is lost, which the compiler guards against in its own code the same way).
  * The sum is bit-identical to the same chain written in plain HIP with the activation in LDS. */
-__device__ __forceinline__ float piece_dot_dpp(uint4 piece, uint4 xq, float xsum) {
+__device__ __forceinline__ float piece_dot_dpp(uint4 piece, uint4 xq, float a0) {
     const uint32_t w[4] = {piece.x, piece.y, piece.z, piece.w};
     uint32_t c[16];
 #pragma unroll
@@ -139,7 +143,7 @@ __device__ __forceinline__ float piece_dot_dpp(uint4 piece, uint4 xq, float xsum
         c[4 * s + 2] = v.z;
         c[4 * s + 3] = v.w;
     }
-    float a = 0.0f;
+    float a = a0;
 #define W4A16_DOT2_DPP(S, X, C)                                                                  \
     "v_dot2c_f32_bf16_dpp %0, " X ", " C " quad_perm:[" S "," S "," S "," S "] row_mask:0xf "   \
     "bank_mask:0xf\n"
@@ -158,7 +162,7 @@ __device__ __forceinline__ float piece_dot_dpp(uint4 piece, uint4 xq, float xsum
                    "v"(c[3]), "v"(c[4]), "v"(c[5]), "v"(c[6]), "v"(c[7]), "v"(c[8]), "v"(c[9]),
                    "v"(c[10]), "v"(c[11]), "v"(c[12]), "v"(c[13]), "v"(c[14]), "v"(c[15]));
 #undef W4A16_DOT2_DPP
-    return fmaf(-0.75f, xsum, a);
+    return a;
 }
 
 /* The sum of the eight BF16 values of a 16-byte chunk as four chained packed dot products with
@@ -170,6 +174,16 @@ __device__ __forceinline__ float chunk_sum8(uint4 v) {
     s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, v.y), one, s, false);
     s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, v.z), one, s, false);
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, v.w), one, s, false);
+}
+
+/* -0.75 times the sum of the 32 activation values a quad of lanes holds (8 a lane): the lane's
+ * chunk sum, then the quad's four lane sums by two DPP adds (each one v_add_f32_dpp). The start
+ * value of a piece's dot chain. */
+__device__ __forceinline__ float quad_offset(uint4 v) {
+    float s8 = chunk_sum8(v);
+    s8 += dpp_f32<kDppQuadSwap1>(s8);
+    s8 += dpp_f32<kDppQuadSwap2>(s8);
+    return -0.75f * s8;
 }
 
 /* SiLU with exp computed as 2^n * 2^(r * log2 e), -g = n ln2 + r, |r| <= ln2/2 (Cody-Waite
@@ -404,7 +418,8 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_tiles_kernel(
             /* one 16-byte chunk a lane: quad lane s reads chunk 4 s + kb of group g, and the
              * dot products take it from there over DPP */
             const uint4 xq = smem4[g * 16 + 4 * (lane & 3) + kb];
-            acc = fmaf(piece_dot_dpp(buf[i], xq, xsum[4 * g + kb]), bf16_widen(sbits[i]), acc);
+            acc = fmaf(piece_dot_dpp(buf[i], xq, -0.75f * xsum[4 * g + kb]), bf16_widen(sbits[i]),
+                       acc);
         }
     }
     acc *= 32.0f; /* piece_dot_dpp returns its sum over 32 */
@@ -540,10 +555,7 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
         if (gw + i * kStride < P) { /* wave-uniform: every lane of the wave takes part */
-            float s8 = chunk_sum8(xv[i]);
-            s8 += dpp_f32<kDppQuadSwap1>(s8);
-            const float xsum = s8 + dpp_f32<kDppQuadSwap2>(s8);
-            acc = fmaf(piece_dot_dpp(buf[i], xv[i], xsum), bf16_widen(sbits[i]), acc);
+            acc = fmaf(piece_dot_dpp(buf[i], xv[i], quad_offset(xv[i])), bf16_widen(sbits[i]), acc);
         }
     }
     acc *= 32.0f; /* piece_dot_dpp returns its sum over 32 */
