@@ -18,6 +18,8 @@
  *   gemv_xwave_kernel   M = 1, long K (the down projection) and K = 1792..3072 (with the
  *                       fused SiLU x up epilogue for gate/up): each wave loads only its own
  *                       pairs' activation, no LDS before the reduction; optional residual epilogue
+ *   gemv_mfma1_kernel   M = 1 on v_mfma_f32_16x16x32_bf16 with a block-diagonal operand (no pair:
+ *                       the C1 down projection's 37 to 48 group pairs, linears of 7 to 10 pairs)
  *   gemv_rows_kernel    2 <= M <= 8: the GEMV's block structure on v_mfma_f32_16x16x32_bf16 with
  *                       a block-diagonal operand, activation loaded straight into LDS
  *   gemv_rows16_kernel  9 <= M <= 16, short K: the same with a tile pair a wave
@@ -493,6 +495,38 @@ __device__ __forceinline__ unsigned split_arrive(unsigned *counter, int lane) {
     return __shfl(prev, 0);
 }
 
+/* The end of an M = 1 GEMV tile: lanes 0-7 hold its eight row sums. PAIR: lane r < 4 has gate
+ * row r and lane r + 4 the matching up row, and lanes 0-3 write BF16(silu(gate) x up); otherwise
+ * eight FP32 or BF16 rows, with the plan-F2 residual update when residual is given. */
+template <bool PAIR, bool OUT_F32>
+__device__ __forceinline__ void gemv_row_epilogue(float row_sum, int lane, int tile, void *out,
+                                                  uint16_t *residual, const uint16_t *sub) {
+    if (PAIR) {
+        /* lane r < 4 has gate row r, lane r + 4 the matching up row (lanes 0-7 are active) */
+        const float upv = dpp_f32<kDppRowShl4>(row_sum);
+        if (lane < 4) {
+            const float gate = bf16_widen(bf16_rne(row_sum));
+            const float up = bf16_widen(bf16_rne(upv));
+            reinterpret_cast<uint16_t *>(out)[tile * 4 + lane] = silu_mul_bf16(gate, up);
+        }
+    } else if (OUT_F32) {
+        reinterpret_cast<float *>(out)[tile * 8 + lane] = row_sum;
+    } else {
+        const int row = tile * 8 + lane;
+        const uint16_t o = bf16_rne(row_sum);
+        if (residual) {
+            /* plan F2 epilogue: residual <- BF16(BF16(residual + sub) + out), the updates of
+             * reference csrc/layer_dispatch.cu:193-209 (this row's inputs are read before
+             * its output is written, so sub may alias out); with no sub the residual already
+             * holds BF16(residual + sub) and only the second update is made */
+            const uint16_t rsum =
+                sub ? (uint16_t)(bf16_add2(residual[row], sub[row]) & 0xFFFFu) : residual[row];
+            residual[row] = (uint16_t)(bf16_add2(rsum, o) & 0xFFFFu);
+        }
+        reinterpret_cast<uint16_t *>(out)[row] = o;
+    }
+}
+
 /* GEMV with wave-local activation: as gemv_tiles_kernel, but each wave loads only the
  * activation of its own group pairs (512 bytes a pair, 8 bytes a lane, issued with its weight
  * loads) into a private LDS slice, and forms the per-(group, kb) sums with shuffles. No block
@@ -584,30 +618,7 @@ __global__ __launch_bounds__(SK * 64) void gemv_xwave_kernel(
         if (lane == 0)
             __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (PAIR) {
-        /* lane r < 4 has gate row r, lane r + 4 the matching up row (lanes 0-7 are active) */
-        const float upv = dpp_f32<kDppRowShl4>(row_sum);
-        if (lane < 4) {
-            const float gate = bf16_widen(bf16_rne(row_sum));
-            const float up = bf16_widen(bf16_rne(upv));
-            reinterpret_cast<uint16_t *>(out)[tile * 4 + lane] = silu_mul_bf16(gate, up);
-        }
-    } else if (OUT_F32) {
-        reinterpret_cast<float *>(out)[tile * 8 + lane] = row_sum;
-    } else {
-        const int row = tile * 8 + lane;
-        const uint16_t o = bf16_rne(row_sum);
-        if (residual) {
-            /* plan F2 epilogue: residual <- BF16(BF16(residual + sub) + out), the updates of
-             * reference csrc/layer_dispatch.cu:193-209 (this row's inputs are read before
-             * its output is written, so sub may alias out); with no sub the residual already
-             * holds BF16(residual + sub) and only the second update is made */
-            const uint16_t rsum =
-                sub ? (uint16_t)(bf16_add2(residual[row], sub[row]) & 0xFFFFu) : residual[row];
-            residual[row] = (uint16_t)(bf16_add2(rsum, o) & 0xFFFFu);
-        }
-        reinterpret_cast<uint16_t *>(out)[row] = o;
-    }
+    gemv_row_epilogue<PAIR, OUT_F32>(row_sum, lane, tile, out, residual, sub);
 }
 
 size_t xwave_smem(int waves, int np) { return (void)np, (size_t)waves * 32; }
@@ -640,6 +651,105 @@ enum { kOutBf16 = 0, kOutPairSilu = 1, kOutF32 = 2 };
 __device__ __forceinline__ bf16x8_t unpack8(uint32_t word) {
     return __builtin_bit_cast(bf16x8_t, code_pairs(word));
 }
+
+
+/* M = 1 on the matrix cores (long K, no pair: the down projection; and the 7-12 pair linears).
+ * The block and wave decomposition of gemv_xwave_kernel (one 8-row tile a block, wave w taking
+ * the group pairs w + SK i), but a pair's products go to v_mfma_f32_16x16x32_bf16 with the
+ * block-diagonal operand of gemv_rows_kernel: lane l loads piece (kb = l / 16, row r = l % 8) of
+ * group 2p + a, a = (l / 8) % 2, which is B column n = 8a + r for k block kb, and A row 0 / 8
+ * carries the activation of group 2p / 2p + 1 (every other row zero), so D[0][r] / D[8][8 + r]
+ * is row r's dot product with group 2p / 2p + 1 (the off-diagonal quadrants mix the groups and are
+ * not read). Four MFMAs a pair, one per piece dword, take B = 0.75 + code/32 from the unpack; a
+ * fifth, issued first, takes the constant -0.75 as B and an A whose rows 0-3 / 8-11 hold the four
+ * 32-value slices of group 2p / 2p + 1, which adds -0.75 times each slice's sum to those rows of
+ * D. The group's result is then D[0] + D[1] + D[2] + D[3] (rows 8-11 for the second group), one
+ * FMA with the scale folds it in, and the VALU does only the unpack and that sum: 33 instructions
+ * a pair against 54 on the v_dot2 path.
+ *
+ * Operands. A wave's activation for pair p (512 bytes, in k order) goes straight into a private
+ * 1 KiB LDS slice by one direct load whose upper 32 lanes read past the buffer, so the slice's
+ * second half is zeros: every A operand is one ds_read_b128 whose address (fixed per lane, the
+ * pair and the k block in the instruction's offset) points into the zeros for the rows that carry
+ * nothing. No block barrier stands before the MFMAs; the SK waves meet in LDS once at the end. */
+template <bool OUT_F32, int SK, int NP>
+__global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
+    const uint16_t *__restrict__ x, const uint8_t *__restrict__ wt,
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, uint16_t *residual,
+    const uint16_t *sub) {
+    extern __shared__ uint4 smem4[];
+    const int G = K >> 7;
+    const int P = (G + 1) >> 1;
+    const int tile = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, kb = lane >> 4;
+    const int a = n >> 3, r = n & 7;
+    uint4 *slice = smem4 + wave * NP * 64; /* NP x 1 KiB: 512 B of activation, then 512 B of zeros */
+    float *red = reinterpret_cast<float *>(smem4 + SK * NP * 64);
+
+    /* 1. the activation of every pair of the wave into its slices, then the weight pieces and
+     * scales (a pair past K reads zeros everywhere) */
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)K * 2);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const uint32_t off = lane < 32 ? (uint32_t)((wave + i * SK) * 512 + lane * 16) : kOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xr, (__attribute__((address_space(3))) void *)(slice + i * 64), 16, off, 0, 0, 0);
+    }
+    const size_t tile_bytes = (size_t)G * 512;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wt + (size_t)tile * tile_bytes, (uint32_t)tile_bytes);
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(st + (size_t)tile * G * 8, (uint32_t)G * 16);
+    uint4 buf[NP];
+    uint16_t sbits[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const int g = 2 * (wave + i * SK) + a;
+        buf[i] = buf_load16_stream(wr, (uint32_t)(g * 512 + (kb * 8 + r) * 16));
+        sbits[i] = buf_load_u16(sr, (uint32_t)(g * 16 + r * 2));
+    }
+    __builtin_amdgcn_s_waitcnt(kVmcntWeights<NP>); /* the activation, loaded first, has landed */
+
+    /* 2. A chunk of a slice: 16 a + 4 s + kb is group 2p + a's k block kb of slice s; 32 + kb
+     * is zeros. cmain: rows 0 and 8 (plus 4 s a dword); coff: rows 0-3 and 8-11, slice = row */
+    const int cmain = n == 0 ? kb : n == 8 ? 16 + kb : 32 + kb;
+    const int coff = n < 4 ? 4 * n + kb : (n >= 8 && n < 12) ? 16 + 4 * (n - 8) + kb : 32 + kb;
+    uint4 offs = make_uint4(0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u); /* BF16 -0.75 */
+    asm volatile("" : "+v"(offs.x), "+v"(offs.y), "+v"(offs.z), "+v"(offs.w)); /* kept in place */
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        if (wave + i * SK < P) { /* wave-uniform */
+            const uint4 *sl = slice + i * 64;
+            f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, sl[coff]),
+                                                        __builtin_bit_cast(bf16x8_t, offs), d, 0, 0, 0);
+            const uint32_t words[4] = {buf[i].x, buf[i].y, buf[i].z, buf[i].w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8_t, sl[cmain + 4 * t]), unpack8(words[t]), d, 0, 0, 0);
+            acc = fmaf((d[0] + d[1]) + (d[2] + d[3]), bf16_widen(sbits[i]), acc);
+        }
+    }
+
+    /* 3. lane r holds row r's sum over group 2p, lane 40 + r over group 2p + 1: after the lane
+     * swap, lane 8 + r holds lane 40 + r's value, which a row rotation by 8 brings to lane r */
+    {
+        float t = acc, u = acc;
+        asm volatile("s_nop 1\n v_permlane32_swap_b32 %0, %1\n s_nop 1" : "+v"(t), "+v"(u));
+        acc += dpp_f32<kDppRowRor8>(u);
+    }
+    if (lane < 8) red[wave * 8 + lane] = acc;
+    __syncthreads();
+    if (wave != 0 || lane >= 8) return;
+    float row_sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < SK; ++w) row_sum += red[w * 8 + lane];
+    gemv_row_epilogue<false, OUT_F32>(32.0f * row_sum, lane, tile, out, residual, sub);
+}
+
+size_t mfma1_smem(int waves, int np) { return (size_t)waves * np * 1024 + (size_t)waves * 32; }
 
 template <int OUT, int XPRE, int MI>
 __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
@@ -1511,6 +1621,17 @@ int launch_xwave_np(const uint16_t *x, const uint8_t *w, const uint16_t *s, void
     return hip_status(hipGetLastError(), "gemv launch");
 }
 
+template <bool OUT_F32, int SK, int NP>
+int launch_mfma1(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N, int K,
+                 hipStream_t stream, uint16_t *residual = nullptr, const uint16_t *sub = nullptr) {
+    if (SK * NP < (K / 128 + 1) / 2)
+        return set_error(W4A16_ERR_CONFIG, "internal: a %d x %d matrix-core gemv shape covers %d of %d "
+                         "group pairs", SK, NP, SK * NP, (K / 128 + 1) / 2);
+    hipLaunchKernelGGL((gemv_mfma1_kernel<OUT_F32, SK, NP>), dim3(N / 8), dim3(SK * 64),
+                       mfma1_smem(SK, NP), stream, x, w, s, out, N, K, residual, sub);
+    return hip_status(hipGetLastError(), "gemv launch");
+}
+
 /* The wave-local kernel for a K of more than kMaxLoads group pairs: up to 48 pairs one block of
  * 16 waves a tile (12 waves at 33 to 36 pairs); beyond, the tile split over BS blocks of 8 waves holding at most 3 pairs each
  * (K = 17408: 12.9 against 13.7 us). residual / sub: the plan-F2 epilogue (BF16 output only).
@@ -1529,6 +1650,11 @@ int launch_xwave(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *o
      * runs, one box) */
     if (pairs > 16 && pairs <= 20)
         return launch_xwave_np<OUT_F32, 2, 10, 1>(x, w, s, out, N, K, stream, residual, sub);
+    /* 37 to 48 pairs (C1's down, K = 9728): the matrix-core form, sixteen waves of three pairs,
+     * C1 11.45 against 11.59-11.70 us for the v_dot2 kernel of the same shape (13 x 3: 11.47,
+     * 10 x 4: 11.61; interleaved runs, one box). At 34 and 68 pairs (C4, C2) the two tie. */
+    if (pairs > 36 && pairs <= 48)
+        return launch_mfma1<OUT_F32, 16, 3>(x, w, s, out, N, K, stream, residual, sub);
     switch ((pairs + kXwaveWaves - 1) / kXwaveWaves) {
         case 1: return launch_xwave_np<OUT_F32, 1, kXwaveWaves, 1>(x, w, s, out, N, K, stream, residual, sub);
         case 2: return launch_xwave_np<OUT_F32, 2, kXwaveWaves, 1>(x, w, s, out, N, K, stream, residual, sub);
@@ -1567,6 +1693,12 @@ int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *ou
         const int st = launch_xwave<OUT_F32>(x, w, s, out, N, K, stream);
         if (st <= 0) return st;
     }
+    /* 7 to 12 pairs without the pair (C0, K = 2560): the matrix-core form, C0 4.30 us at five
+     * waves of two pairs against 4.51 for the v_dot2 kernel's four of three (4 x 3: 4.40, 6 x 3,
+     * 8 x 2, 10 x 2, 4 x 4: 4.56-5.72); for gate/up (the pair) the two tie, and the v_dot2 kernel
+     * stays */
+    if (!PAIR && !norm && pairs > 6 && pairs <= 10) return launch_mfma1<OUT_F32, 5, 2>(x, w, s, out, N, K, stream);
+    if (!PAIR && !norm && pairs > 10 && pairs <= 12) return launch_mfma1<OUT_F32, 4, 3>(x, w, s, out, N, K, stream);
     if (!norm && pairs > 6 && pairs <= 12)
         return launch_xwave_np<OUT_F32, 3, 4, 1, PAIR>(x, w, s, out, N, K, stream);
     if (norm) {

@@ -107,9 +107,13 @@ def test_quantize_device_bit_exact(cuda):
                                  (64, 49152),
                                  # wave-local kernel, one pair a wave, 288 and 384 tiles
                                  (2304, 4096), (3072, 4096),
-                                 # 7 to 12 group pairs: four waves of three pairs a tile,
-                                 # including odd group counts
+                                 # 7 to 12 group pairs: the matrix-core kernel, five waves of
+                                 # two pairs (7-10) and four of three (11-12) a tile, including
+                                 # odd group counts
                                  (64, 1792), (64, 2816), (40, 3072), (16, 2944), (56, 1920),
+                                 # 37 to 48 pairs: the matrix-core kernel, sixteen waves of
+                                 # three pairs (75 groups is odd)
+                                 (64, 9472), (48, 9600), (32, 12288),
                                  # 33 to 36 pairs: twelve waves of three pairs a tile
                                  (512, 8448 + 128), (128, 8704), (64, 9216),
                                  # 17 to 20 pairs: ten waves of two pairs a tile (the
