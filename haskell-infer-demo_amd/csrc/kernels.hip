@@ -18,8 +18,9 @@
  *   gemv_xwave_kernel   M = 1, long K (the down projection) and K = 1792..3072 (with the
  *                       fused SiLU x up epilogue for gate/up): each wave loads only its own
  *                       pairs' activation, no LDS before the reduction; optional residual epilogue
- *   gemv_mfma1_kernel   M = 1 on v_mfma_f32_16x16x32_bf16 with a block-diagonal operand (no pair:
- *                       the C1 down projection's 37 to 48 group pairs, linears of 7 to 10 pairs)
+ *   gemv_mfma1_kernel   M = 1 or 2 on v_mfma_f32_16x16x32_bf16 with a block-diagonal operand, one
+ *                       tile a block, wave-local activation: the C1 down projection's 37 to 48
+ *                       group pairs, linears of 7 to 12 pairs, and at M = 2 the gate/up pair
  *   gemv_rows_kernel    2 <= M <= 8: the GEMV's block structure on v_mfma_f32_16x16x32_bf16 with
  *                       a block-diagonal operand, activation loaded straight into LDS
  *   gemv_rows16_kernel  9 <= M <= 16, short K: the same with a tile pair a wave
@@ -495,24 +496,26 @@ __device__ __forceinline__ unsigned split_arrive(unsigned *counter, int lane) {
     return __shfl(prev, 0);
 }
 
-/* The end of an M = 1 GEMV tile: lanes 0-7 hold its eight row sums. PAIR: lane r < 4 has gate
- * row r and lane r + 4 the matching up row, and lanes 0-3 write BF16(silu(gate) x up); otherwise
- * eight FP32 or BF16 rows, with the plan-F2 residual update when residual is given. */
+/* The end of an M = 1 GEMV tile: eight lanes (one DPP row of sixteen, in order) hold its eight
+ * row sums, row r on the lane this call passes r. PAIR: row r < 4 is gate row r and row r + 4
+ * the matching up row, and the lanes of r < 4 write BF16(silu(gate) x up); otherwise eight FP32
+ * or BF16 rows, with the plan-F2 residual update when residual is given. */
 template <bool PAIR, bool OUT_F32>
-__device__ __forceinline__ void gemv_row_epilogue(float row_sum, int lane, int tile, void *out,
+__device__ __forceinline__ void gemv_row_epilogue(float row_sum, int r, int tile, void *out,
                                                   uint16_t *residual, const uint16_t *sub) {
     if (PAIR) {
-        /* lane r < 4 has gate row r, lane r + 4 the matching up row (lanes 0-7 are active) */
+        /* row r < 4 is gate row r, r + 4 the matching up row, four lanes further in the same
+         * row of sixteen lanes */
         const float upv = dpp_f32<kDppRowShl4>(row_sum);
-        if (lane < 4) {
+        if (r < 4) {
             const float gate = bf16_widen(bf16_rne(row_sum));
             const float up = bf16_widen(bf16_rne(upv));
-            reinterpret_cast<uint16_t *>(out)[tile * 4 + lane] = silu_mul_bf16(gate, up);
+            reinterpret_cast<uint16_t *>(out)[tile * 4 + r] = silu_mul_bf16(gate, up);
         }
     } else if (OUT_F32) {
-        reinterpret_cast<float *>(out)[tile * 8 + lane] = row_sum;
+        reinterpret_cast<float *>(out)[tile * 8 + r] = row_sum;
     } else {
-        const int row = tile * 8 + lane;
+        const int row = tile * 8 + r;
         const uint16_t o = bf16_rne(row_sum);
         if (residual) {
             /* plan F2 epilogue: residual <- BF16(BF16(residual + sub) + out), the updates of
@@ -653,30 +656,33 @@ __device__ __forceinline__ bf16x8_t unpack8(uint32_t word) {
 }
 
 
-/* M = 1 on the matrix cores (long K, no pair: the down projection; and the 7-12 pair linears).
- * The block and wave decomposition of gemv_xwave_kernel (one 8-row tile a block, wave w taking
- * the group pairs w + SK i), but a pair's products go to v_mfma_f32_16x16x32_bf16 with the
- * block-diagonal operand of gemv_rows_kernel: lane l loads piece (kb = l / 16, row r = l % 8) of
- * group 2p + a, a = (l / 8) % 2, which is B column n = 8a + r for k block kb, and A row 0 / 8
- * carries the activation of group 2p / 2p + 1 (every other row zero), so D[0][r] / D[8][8 + r]
- * is row r's dot product with group 2p / 2p + 1 (the off-diagonal quadrants mix the groups and are
- * not read). Four MFMAs a pair, one per piece dword, take B = 0.75 + code/32 from the unpack; a
- * fifth, issued first, takes the constant -0.75 as B and an A whose rows 0-3 / 8-11 hold the four
- * 32-value slices of group 2p / 2p + 1, which adds -0.75 times each slice's sum to those rows of
- * D. The group's result is then D[0] + D[1] + D[2] + D[3] (rows 8-11 for the second group), one
- * FMA with the scale folds it in, and the VALU does only the unpack and that sum: 33 instructions
- * a pair against 54 on the v_dot2 path.
+/* M = 1 or 2 rows on the matrix cores. The block and wave decomposition of gemv_xwave_kernel (one
+ * 8-row tile a block, wave w taking the group pairs w + SK i), but a pair's products go to
+ * v_mfma_f32_16x16x32_bf16 with a block-diagonal operand: lane l loads piece (kb = l / 16,
+ * row r = l % 8) of group 2p + a, a = (l / 8) % 2, which is B column n = 8a + r for k block kb,
+ * and A row 8a + 4t carries activation row t (t < M) of group 2p + a, every other row zero, so
+ * D[8a + 4t][8a + r] is row r's dot product with activation row t over group 2p + a (the
+ * off-diagonal quadrants mix the groups and are not read). Four MFMAs a pair, one per piece
+ * dword, take B = 0.75 + code/32 from the unpack; a fifth, issued first, takes the constant
+ * -0.75 as B and an A whose row 8a + 4t + s holds slice s (the 32 values of k block s of every
+ * kb) of activation row t over group 2p + a, which adds -0.75 times each slice's sum to those
+ * rows of D. Rows 8a + 4t .. 8a + 4t + 3 of D sit in the four accumulator registers of lane
+ * 16 (2a + t) + n, so the group's result is the sum of that lane's four registers, and one FMA
+ * with the scale folds it in: the VALU does only the unpack and that sum (33 instructions a pair
+ * against 54 on the v_dot2 path, whatever M).
  *
- * Operands. A wave's activation for pair p (512 bytes, in k order) goes straight into a private
- * 1 KiB LDS slice by one direct load whose upper 32 lanes read past the buffer, so the slice's
- * second half is zeros: every A operand is one ds_read_b128 whose address (fixed per lane, the
- * pair and the k block in the instruction's offset) points into the zeros for the rows that carry
- * nothing. No block barrier stands before the MFMAs; the SK waves meet in LDS once at the end. */
-template <bool OUT_F32, int SK, int NP>
+ * Operands. A wave's activation for pair p (M x 512 bytes, in k order) goes straight into a
+ * private 1 KiB LDS slice by one direct load (lanes 0-31 row 0; lanes 32-63 row 1 when M = 2,
+ * otherwise past the buffer, so that half holds zeros), and a 256-byte zero area after each slice
+ * serves the rows that carry nothing: every A operand is one ds_read_b128 whose address is fixed per
+ * lane (the pair and the k block in the instruction's offset). No block barrier stands before
+ * the MFMAs; the SK waves meet in LDS once at the end. */
+template <bool PAIR, bool OUT_F32, int SK, int NP, int M>
 __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ wt,
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, uint16_t *residual,
     const uint16_t *sub) {
+    static_assert(M == 1 || M == 2, "one or two activation rows");
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
     const int P = (G + 1) >> 1;
@@ -685,17 +691,23 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, kb = lane >> 4;
     const int a = n >> 3, r = n & 7;
-    uint4 *slice = smem4 + wave * NP * 64; /* NP x 1 KiB: 512 B of activation, then 512 B of zeros */
-    float *red = reinterpret_cast<float *>(smem4 + SK * NP * 64);
+    uint4 *slice = smem4 + wave * NP * 80; /* per pair 1 KiB of activation, then 256 B of zeros */
+    float *red = reinterpret_cast<float *>(smem4 + SK * NP * 80);
 
-    /* 1. the activation of every pair of the wave into its slices, then the weight pieces and
-     * scales (a pair past K reads zeros everywhere) */
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)K * 2);
+    /* 1. the zero areas, the activation of every pair of the wave into its slices, then the
+     * weight pieces and scales (a pair past K reads zeros everywhere) */
+#pragma unroll
+    for (int i = 0; i < NP; ++i) reinterpret_cast<uint32_t *>(slice + i * 80 + 64)[lane] = 0u;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)K * 2 * M);
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-        const uint32_t off = lane < 32 ? (uint32_t)((wave + i * SK) * 512 + lane * 16) : kOob;
+        const int c = (wave + i * SK) * 512 + (lane & 31) * 16; /* byte of k within a row */
+        const uint32_t off = c >= K * 2 ? kOob
+                             : lane < 32 ? (uint32_t)c
+                             : M == 2    ? (uint32_t)(K * 2 + c)
+                                         : kOob;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            xr, (__attribute__((address_space(3))) void *)(slice + i * 64), 16, off, 0, 0, 0);
+            xr, (__attribute__((address_space(3))) void *)(slice + i * 80), 16, off, 0, 0, 0);
     }
     const size_t tile_bytes = (size_t)G * 512;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wt + (size_t)tile * tile_bytes, (uint32_t)tile_bytes);
@@ -710,17 +722,19 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
     }
     __builtin_amdgcn_s_waitcnt(kVmcntWeights<NP>); /* the activation, loaded first, has landed */
 
-    /* 2. A chunk of a slice: 16 a + 4 s + kb is group 2p + a's k block kb of slice s; 32 + kb
-     * is zeros. cmain: rows 0 and 8 (plus 4 s a dword); coff: rows 0-3 and 8-11, slice = row */
-    const int cmain = n == 0 ? kb : n == 8 ? 16 + kb : 32 + kb;
-    const int coff = n < 4 ? 4 * n + kb : (n >= 8 && n < 12) ? 16 + 4 * (n - 8) + kb : 32 + kb;
+    /* 2. A chunks: 32 t + 16 a + 4 s + kb of a slice is row t's k block kb of slice s of group
+     * 2p + a; the pair's zero area is 64 chunks on. cmain: row 8a + 4t (plus 4 s a dword); coff: row
+     * 8a + 4t + s */
+    const int ta = (n >> 2) & 1;
+    const int cmain = (n & 3) == 0 && ta < M ? 32 * ta + 16 * a + kb : 64 + kb;
+    const int coff = ta < M ? 32 * ta + 16 * a + 4 * (n & 3) + kb : 64 + kb;
     uint4 offs = make_uint4(0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u); /* BF16 -0.75 */
     asm volatile("" : "+v"(offs.x), "+v"(offs.y), "+v"(offs.z), "+v"(offs.w)); /* kept in place */
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
         if (wave + i * SK < P) { /* wave-uniform */
-            const uint4 *sl = slice + i * 64;
+            const uint4 *sl = slice + i * 80;
             f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
             d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, sl[coff]),
                                                         __builtin_bit_cast(bf16x8_t, offs), d, 0, 0, 0);
@@ -730,26 +744,40 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
                 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                     __builtin_bit_cast(bf16x8_t, sl[cmain + 4 * t]), unpack8(words[t]), d, 0, 0, 0);
             acc = fmaf((d[0] + d[1]) + (d[2] + d[3]), bf16_widen(sbits[i]), acc);
+        } else {
+            /* a use on this path too, so the compiler keeps the pair's loads ahead of the branch
+             * (sunk into it, they would be issued after the wait above, which then no longer
+             * covers the activation) */
+            asm volatile("" ::"v"(buf[i].x), "v"(sbits[i]));
         }
     }
 
-    /* 3. lane r holds row r's sum over group 2p, lane 40 + r over group 2p + 1: after the lane
-     * swap, lane 8 + r holds lane 40 + r's value, which a row rotation by 8 brings to lane r */
+    /* 3. lane 16 t + r holds row r's sum for activation row t over group 2p, lane 40 + 16 t + r
+     * over group 2p + 1: after the lane swap, lane 8 + 16 t + r holds the latter, which a row
+     * rotation by 8 brings to lane 16 t + r */
     {
         float t = acc, u = acc;
         asm volatile("s_nop 1\n v_permlane32_swap_b32 %0, %1\n s_nop 1" : "+v"(t), "+v"(u));
         acc += dpp_f32<kDppRowRor8>(u);
     }
-    if (lane < 8) red[wave * 8 + lane] = acc;
+    const int trow = lane >> 4;
+    if (r == n && trow < M) red[(wave * M + trow) * 8 + r] = acc;
     __syncthreads();
-    if (wave != 0 || lane >= 8) return;
+    if (wave != 0 || lane >= 8 * M) return;
+    /* lane 8 t + r finishes row r of activation row t (rows r and r + 4 in one DPP row) */
+    const int t = lane >> 3, rr = lane & 7;
     float row_sum = 0.0f;
 #pragma unroll
-    for (int w = 0; w < SK; ++w) row_sum += red[w * 8 + lane];
-    gemv_row_epilogue<false, OUT_F32>(32.0f * row_sum, lane, tile, out, residual, sub);
+    for (int w = 0; w < SK; ++w) row_sum += red[(w * M + t) * 8 + rr];
+    const size_t ocols = PAIR ? (size_t)N / 2 : (size_t)N;
+    void *out_t = OUT_F32 ? (void *)(reinterpret_cast<float *>(out) + t * ocols)
+                          : (void *)(reinterpret_cast<uint16_t *>(out) + t * ocols);
+    gemv_row_epilogue<PAIR, OUT_F32>(32.0f * row_sum, rr, tile, out_t,
+                                     residual ? residual + t * ocols : nullptr,
+                                     sub ? sub + t * ocols : nullptr);
 }
 
-size_t mfma1_smem(int waves, int np) { return (size_t)waves * np * 1024 + (size_t)waves * 32; }
+size_t mfma1_smem(int waves, int np) { return (size_t)waves * np * 1280 + (size_t)waves * 64; }
 
 template <int OUT, int XPRE, int MI>
 __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
@@ -1621,13 +1649,13 @@ int launch_xwave_np(const uint16_t *x, const uint8_t *w, const uint16_t *s, void
     return hip_status(hipGetLastError(), "gemv launch");
 }
 
-template <bool OUT_F32, int SK, int NP>
+template <bool OUT_F32, int SK, int NP, bool PAIR = false, int M = 1>
 int launch_mfma1(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *out, int N, int K,
                  hipStream_t stream, uint16_t *residual = nullptr, const uint16_t *sub = nullptr) {
     if (SK * NP < (K / 128 + 1) / 2)
         return set_error(W4A16_ERR_CONFIG, "internal: a %d x %d matrix-core gemv shape covers %d of %d "
                          "group pairs", SK, NP, SK * NP, (K / 128 + 1) / 2);
-    hipLaunchKernelGGL((gemv_mfma1_kernel<OUT_F32, SK, NP>), dim3(N / 8), dim3(SK * 64),
+    hipLaunchKernelGGL((gemv_mfma1_kernel<PAIR, OUT_F32, SK, NP, M>), dim3(N / 8), dim3(SK * 64),
                        mfma1_smem(SK, NP), stream, x, w, s, out, N, K, residual, sub);
     return hip_status(hipGetLastError(), "gemv launch");
 }
@@ -1839,6 +1867,17 @@ int launch_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, v
         return launch_rows16<PAIR, OUT_F32>(x, M, w, s, out, N, K, stream, cm);
     if (M < 2 || M > 8) return 1;
     const int pairs = (K / 128 + 1) / 2;
+    /* two rows on the matrix-core GEMV: the gate/up pair at 7 to 12 group pairs (four waves of
+     * three) and the long K of the C1 down projection, 37 to 48 pairs (sixteen of three). Whole
+     * C1 FFN call at M = 2: 12.58-12.66 us against 13.70-13.99 on this kernel's few-row form
+     * (down alone 12.82-12.90, gate/up alone 13.55; gate/up as five waves of two ties; down as
+     * thirteen of three 12.58 with the gate/up; interleaved runs, one box). */
+    if (M == 2 && !norm && !cm) {
+        if (PAIR && pairs > 6 && pairs <= 12)
+            return launch_mfma1<OUT_F32, 4, 3, true, 2>(x, w, s, out, N, K, stream);
+        if (!PAIR && pairs > 36 && pairs <= 48)
+            return launch_mfma1<OUT_F32, 16, 3, false, 2>(x, w, s, out, N, K, stream, residual);
+    }
     if (pairs <= 12 && M <= 4) {
         if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 4, 1, 3>(x, M, w, s, out, N, K, stream, norm, residual, cm);
         if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 3>(x, M, w, s, out, N, K, stream, norm, residual, cm);

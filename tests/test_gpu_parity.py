@@ -157,14 +157,24 @@ def test_few_rows_parity(cuda, m):
         w = w4a16.TiledWeight.from_artifact(p, s, n, k, device=cuda)
         out = from_dev(w4a16.gemm_int4_bf16(to_dev(x, cuda), w))
         assert_parity(out, oracle.gemm_bf16(x, p, s, n, k), f"gemm M={m} {n}x{k}")
-    hidden, inter = 1152, 72
-    say(f"gate/up M={m} H={hidden} I={inter}")
-    gp, gs = make_weight(2 * inter, hidden, seed=300 + m)
-    x = oracle.synth_activation(m, hidden, seed=400 + m)
-    gu = w4a16.TiledWeight.from_artifact(gp, gs, 2 * inter, hidden, pair=True, device=cuda)
-    act = from_dev(w4a16.gate_up_silu(to_dev(x, cuda), gu))
-    mid = oracle.gemm_bf16(x, gp, gs, 2 * inter, hidden)
-    assert_parity(act, oracle.silu_mul_packed(mid, m, inter), f"gate/up M={m}")
+    # the gate/up pair at an odd group count; at M = 2 also on the matrix-core GEMV (7 to 12
+    # group pairs, 23 groups odd), whose long-K down form the 38-pair shape above takes
+    for hidden, inter in [(1152, 72)] + ([(2944, 72), (1792, 40)] if m == 2 else []):
+        say(f"gate/up M={m} H={hidden} I={inter}")
+        gp, gs = make_weight(2 * inter, hidden, seed=300 + m + hidden)
+        x = oracle.synth_activation(m, hidden, seed=400 + m)
+        gu = w4a16.TiledWeight.from_artifact(gp, gs, 2 * inter, hidden, pair=True, device=cuda)
+        act = from_dev(w4a16.gate_up_silu(to_dev(x, cuda), gu))
+        mid = oracle.gemm_bf16(x, gp, gs, 2 * inter, hidden)
+        assert_parity(act, oracle.silu_mul_packed(mid, m, inter), f"gate/up M={m} H={hidden}")
+    if m == 2:
+        n, k = 48, 9600  # 75 groups: the last pair's second group past K
+        say(f"gemm M={m} n={n} k={k}")
+        p, s = make_weight(n, k, seed=n + k + m)
+        x = oracle.synth_activation(m, k, seed=200 + m)
+        w = w4a16.TiledWeight.from_artifact(p, s, n, k, device=cuda)
+        out = from_dev(w4a16.gemm_int4_bf16(to_dev(x, cuda), w))
+        assert_parity(out, oracle.gemm_bf16(x, p, s, n, k), f"gemm M={m} {n}x{k}")
 
 
 def test_random_shapes_parity(cuda):
@@ -433,11 +443,12 @@ def test_ffn_norm_parity(cuda, style, m):
 
 @pytest.mark.parametrize("m", [2, 3, 5, 8])
 def test_ffn_norm_fused_rows(cuda, m):
-    """mlp_int4_norm for 2 <= M <= 8 against the explicit composition, bit-identical act and
-    output for both norm styles: at M = 2 the few-row kernel's own prologue, whose FP64 sum of
-    squares gives the correctly rounded scale, against the oracle's RMSNorm (FP64 scale, FP32
-    products) followed by the fused gate/up; from M = 3 the standalone RMSNorm then the fused
-    gate/up. Within rel-L2 1e-3 of the oracle end to end. (Against the oracle's per-element bar
+    """mlp_int4_norm for 2 <= M <= 8 against the explicit composition, for both norm styles: at
+    M = 2 the few-row kernel's own prologue, whose FP64 sum of squares gives the correctly
+    rounded scale, against the oracle's RMSNorm (FP64 scale, FP32 products) followed by the
+    fused gate/up (another kernel at M = 2, the matrix-core GEMV: act to the parity bar, then
+    the down projection bit-identical on the fused call's own act); from M = 3 the standalone
+    RMSNorm then the fused gate/up, act and output bit-identical. Within rel-L2 1e-3 of the oracle end to end. (Against the oracle's per-element bar
     these residual inputs leave a few act values at 3 BF16 ULP at M = 5 and 8: one normalised
     value rounded the other way by the FP32 norm moves every gate/up sum.)"""
     import torch
@@ -458,7 +469,11 @@ def test_ffn_norm_fused_rows(cuda, m):
         else:
             normed = w4a16.rmsnorm(xd, wd, style, 1e-6)
         act2 = w4a16.gate_up_silu(normed, gu)
-        assert np.array_equal(act, from_dev(act2)), (m, style)
+        if m == 2:  # the prologue's few-row kernel against the matrix-core gate/up of M = 2
+            assert_parity(act, from_dev(act2), f"norm gate/up M={m} against its two stages")
+            act2 = to_dev(act, cuda)  # the down kernel checked on the fused call's own act
+        else:
+            assert np.array_equal(act, from_dev(act2)), (m, style)
         down2 = from_dev(w4a16.gemm_int4_bf16(act2, dn))
         if m < 4 or m >= 8:  # the same down kernel and summation order
             assert np.array_equal(out, down2), (m, style)
