@@ -673,8 +673,8 @@ __device__ __forceinline__ bf16x8_t unpack8(uint32_t word) {
  *
  * Operands. A wave's activation for pair p (M x 512 bytes, in k order) goes straight into a
  * private 1 KiB LDS slice by one direct load (lanes 0-31 row 0; lanes 32-63 row 1 when M = 2,
- * otherwise past the buffer, so that half holds zeros), and a 256-byte zero area after each slice
- * serves the rows that carry nothing: every A operand is one ds_read_b128 whose address is fixed per
+ * otherwise past the buffer, so that half holds zeros), and at M = 2 a 256-byte zero area after
+ * each slice serves the rows that carry nothing: every A operand is one ds_read_b128 whose address is fixed per
  * lane (the pair and the k block in the instruction's offset). No block barrier stands before
  * the MFMAs; the SK waves meet in LDS once at the end. */
 template <bool PAIR, bool OUT_F32, int SK, int NP, int M>
@@ -683,6 +683,11 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, uint16_t *residual,
     const uint16_t *sub) {
     static_assert(M == 1 || M == 2, "one or two activation rows");
+    /* a pair's slice in 16-byte chunks: 1 KiB of rows, then at M = 2 256 bytes of zeros; its
+     * zero chunks: M = 1 the second half (the direct load's lanes past the buffer), M = 2 the
+     * area after it */
+    constexpr int STRIDE = M == 2 ? 80 : 64;
+    constexpr int ZERO = M == 2 ? 64 : 32;
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
     const int P = (G + 1) >> 1;
@@ -691,13 +696,15 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, kb = lane >> 4;
     const int a = n >> 3, r = n & 7;
-    uint4 *slice = smem4 + wave * NP * 80; /* per pair 1 KiB of activation, then 256 B of zeros */
-    float *red = reinterpret_cast<float *>(smem4 + SK * NP * 80);
+    uint4 *slice = smem4 + wave * NP * STRIDE;
+    float *red = reinterpret_cast<float *>(smem4 + SK * NP * STRIDE);
 
     /* 1. the zero areas, the activation of every pair of the wave into its slices, then the
      * weight pieces and scales (a pair past K reads zeros everywhere) */
+    if (M == 2) {
 #pragma unroll
-    for (int i = 0; i < NP; ++i) reinterpret_cast<uint32_t *>(slice + i * 80 + 64)[lane] = 0u;
+        for (int i = 0; i < NP; ++i) reinterpret_cast<uint32_t *>(slice + i * STRIDE + 64)[lane] = 0u;
+    }
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)K * 2 * M);
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
@@ -707,7 +714,7 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
                              : M == 2    ? (uint32_t)(K * 2 + c)
                                          : kOob;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            xr, (__attribute__((address_space(3))) void *)(slice + i * 80), 16, off, 0, 0, 0);
+            xr, (__attribute__((address_space(3))) void *)(slice + i * STRIDE), 16, off, 0, 0, 0);
     }
     const size_t tile_bytes = (size_t)G * 512;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wt + (size_t)tile * tile_bytes, (uint32_t)tile_bytes);
@@ -723,18 +730,18 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
     __builtin_amdgcn_s_waitcnt(kVmcntWeights<NP>); /* the activation, loaded first, has landed */
 
     /* 2. A chunks: 32 t + 16 a + 4 s + kb of a slice is row t's k block kb of slice s of group
-     * 2p + a; the pair's zero area is 64 chunks on. cmain: row 8a + 4t (plus 4 s a dword); coff: row
+     * 2p + a; ZERO + kb reads zeros. cmain: row 8a + 4t (plus 4 s a dword); coff: row
      * 8a + 4t + s */
     const int ta = (n >> 2) & 1;
-    const int cmain = (n & 3) == 0 && ta < M ? 32 * ta + 16 * a + kb : 64 + kb;
-    const int coff = ta < M ? 32 * ta + 16 * a + 4 * (n & 3) + kb : 64 + kb;
+    const int cmain = (n & 3) == 0 && ta < M ? 32 * ta + 16 * a + kb : ZERO + kb;
+    const int coff = ta < M ? 32 * ta + 16 * a + 4 * (n & 3) + kb : ZERO + kb;
     uint4 offs = make_uint4(0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u); /* BF16 -0.75 */
     asm volatile("" : "+v"(offs.x), "+v"(offs.y), "+v"(offs.z), "+v"(offs.w)); /* kept in place */
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
         if (wave + i * SK < P) { /* wave-uniform */
-            const uint4 *sl = slice + i * 80;
+            const uint4 *sl = slice + i * STRIDE;
             f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
             d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, sl[coff]),
                                                         __builtin_bit_cast(bf16x8_t, offs), d, 0, 0, 0);
@@ -777,7 +784,9 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
                                      sub ? sub + t * ocols : nullptr);
 }
 
-size_t mfma1_smem(int waves, int np) { return (size_t)waves * np * 1280 + (size_t)waves * 64; }
+size_t mfma1_smem(int waves, int np, int m) {
+    return (size_t)waves * np * (m == 2 ? 1280 : 1024) + (size_t)waves * 64;
+}
 
 template <int OUT, int XPRE, int MI>
 __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
@@ -1656,7 +1665,7 @@ int launch_mfma1(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *o
         return set_error(W4A16_ERR_CONFIG, "internal: a %d x %d matrix-core gemv shape covers %d of %d "
                          "group pairs", SK, NP, SK * NP, (K / 128 + 1) / 2);
     hipLaunchKernelGGL((gemv_mfma1_kernel<PAIR, OUT_F32, SK, NP, M>), dim3(N / 8), dim3(SK * 64),
-                       mfma1_smem(SK, NP), stream, x, w, s, out, N, K, residual, sub);
+                       mfma1_smem(SK, NP, M), stream, x, w, s, out, N, K, residual, sub);
     return hip_status(hipGetLastError(), "gemv launch");
 }
 
