@@ -708,11 +708,7 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)K * 2 * M);
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-        /* lane l fills LDS chunk l: row t = l / 32, group half a = (l / 16) % 2, and the
-         * chunk 16 a + (c ^ (a + 2 t)) of the pair's row, c = l % 16 (swizzled: the A rows read
-         * together then sit in different banks) */
-        const int sw = ((lane >> 4) & 1) + 2 * (lane >> 5);
-        const int c = (wave + i * SK) * 512 + (lane & 16) * 16 + ((lane & 15) ^ sw) * 16;
+        const int c = (wave + i * SK) * 512 + (lane & 31) * 16; /* byte of k within a row */
         const uint32_t off = c >= K * 2 ? kOob
                              : lane < 32 ? (uint32_t)c
                              : M == 2    ? (uint32_t)(K * 2 + c)
@@ -733,13 +729,12 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
     }
     __builtin_amdgcn_s_waitcnt(kVmcntWeights<NP>); /* the activation, loaded first, has landed */
 
-    /* 2. A chunks: 32 t + 16 a + 4 s + (kb ^ (a + 2 t)) of a slice is row t's k block kb of
-     * slice s of group 2p + a; ZERO + kb reads zeros. cmain: row 8a + 4t (plus 4 s a dword); coff: row
+    /* 2. A chunks: 32 t + 16 a + 4 s + kb of a slice is row t's k block kb of slice s of group
+     * 2p + a; ZERO + kb reads zeros. cmain: row 8a + 4t (plus 4 s a dword); coff: row
      * 8a + 4t + s */
     const int ta = (n >> 2) & 1;
-    const int kbs = kb ^ (a + 2 * ta); /* the staging swizzle */
-    const int cmain = (n & 3) == 0 && ta < M ? 32 * ta + 16 * a + kbs : ZERO + kb;
-    const int coff = ta < M ? 32 * ta + 16 * a + 4 * (n & 3) + kbs : ZERO + kb;
+    const int cmain = (n & 3) == 0 && ta < M ? 32 * ta + 16 * a + kb : ZERO + kb;
+    const int coff = ta < M ? 32 * ta + 16 * a + 4 * (n & 3) + kb : ZERO + kb;
     uint4 offs = make_uint4(0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u); /* BF16 -0.75 */
     asm volatile("" : "+v"(offs.x), "+v"(offs.y), "+v"(offs.z), "+v"(offs.w)); /* kept in place */
     float acc = 0.0f;
