@@ -20,7 +20,8 @@
  *                       pairs' activation, no LDS before the reduction; optional residual epilogue
  *   gemv_mfma1_kernel   M = 1 or 2 on v_mfma_f32_16x16x32_bf16 with a block-diagonal operand, one
  *                       tile a block, wave-local activation: the C1 down projection's 37 to 48
- *                       group pairs, linears of 7 to 12 pairs, and at M = 2 the gate/up pair
+ *                       group pairs, linears of 7 to 12 and 17 to 20 pairs, and at M = 2 the
+ *                       gate/up pair
  *   gemv_rows_kernel    2 <= M <= 8: the GEMV's block structure on v_mfma_f32_16x16x32_bf16 with
  *                       a block-diagonal operand, activation loaded straight into LDS
  *   gemv_rows16_kernel  9 <= M <= 16, short K: the same with a tile pair a wave
@@ -1682,11 +1683,12 @@ int launch_xwave(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *o
      * pairs (C1's down) thirteen waves only tie sixteen. */
     if (pairs > 32 && pairs <= 36)
         return launch_xwave_np<OUT_F32, 3, 12, 1>(x, w, s, out, N, K, stream, residual, sub);
-    /* 17 to 20 pairs (C5, K = 5120): ten waves of two pairs, 4.10 against 4.21 us for sixteen
-     * waves of which twelve held one pair (3 x 7: 4.17, 4 x 5: 4.35, 5 x 4: 4.43; interleaved
-     * runs, one box) */
+    /* 17 to 20 pairs (C5, K = 5120): the matrix-core form, ten waves of two pairs, 4.02 us
+     * against 4.09-4.10 for the v_dot2 kernel of the same shape (matrix-core 7 x 3: 4.16, 5 x 4:
+     * 4.27; the v_dot2 kernel: 16 waves of which twelve held one pair 4.21, 3 x 7 4.17, 4 x 5
+     * 4.35, 5 x 4 4.43; interleaved runs, one box) */
     if (pairs > 16 && pairs <= 20)
-        return launch_xwave_np<OUT_F32, 2, 10, 1>(x, w, s, out, N, K, stream, residual, sub);
+        return launch_mfma1<OUT_F32, 10, 2>(x, w, s, out, N, K, stream, residual, sub);
     /* 37 to 48 pairs (C1's down, K = 9728): the matrix-core form, sixteen waves of three pairs,
      * C1 11.45 against 11.59-11.70 us for the v_dot2 kernel of the same shape (13 x 3: 11.47,
      * 10 x 4: 11.61; interleaved runs, one box). At 34 and 68 pairs (C4, C2) the two tie. */
