@@ -1744,10 +1744,13 @@ int launch_xwave(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *o
      * 4.35, 5 x 4 4.43; interleaved runs, one box) */
     if (pairs > 16 && pairs <= 20)
         return launch_mfma1<OUT_F32, 10, 2>(x, w, s, out, N, K, stream, residual, sub);
-    /* 37 to 48 pairs (C1's down, K = 9728): the matrix-core form, sixteen waves of three pairs,
-     * C1 11.45 against 11.59-11.70 us for the v_dot2 kernel of the same shape (13 x 3: 11.47,
-     * 10 x 4: 11.61; interleaved runs, one box). At 34 and 68 pairs (C4, C2) the two tie. */
-    if (pairs > 36 && pairs <= 48)
+    /* 37 to 48 pairs (C1's down, K = 9728): the matrix-core form, C1 11.45 against 11.59-11.70
+     * us for the v_dot2 kernel of the same shape; thirteen waves of three pairs up to 39 pairs
+     * (11.31-11.36 against 11.37-11.44 for sixteen, 10 x 4: 11.54-11.58; three interleaved runs,
+     * one box), sixteen beyond. At 34 and 68 pairs (C4, C2) the two forms tie. */
+    if (pairs > 36 && pairs <= 39)
+        return launch_mfma1<OUT_F32, 13, 3>(x, w, s, out, N, K, stream, residual, sub);
+    if (pairs > 39 && pairs <= 48)
         return launch_mfma1<OUT_F32, 16, 3>(x, w, s, out, N, K, stream, residual, sub);
     switch ((pairs + kXwaveWaves - 1) / kXwaveWaves) {
         case 1: return launch_xwave_np<OUT_F32, 1, kXwaveWaves, 1>(x, w, s, out, N, K, stream, residual, sub);
