@@ -269,6 +269,20 @@ __device__ __forceinline__ int div_small(int u, uint32_t magic) {
 template <int NL>
 constexpr int kVmcntWeights = ((2 * NL) & 15) | (7 << 4) | (15 << 8) | (((2 * NL) >> 4) << 14);
 
+/* s_waitcnt "at most C - 2 i vector memory operations outstanding" for an unrolled loop index i
+ * (the builtin takes only a constant; i >= 4 waits for everything) */
+constexpr int vm_enc(int c) { return (c & 15) | (7 << 4) | (15 << 8) | ((c >> 4) << 14); }
+template <int C>
+__device__ __forceinline__ void wait_vm(int i) {
+    switch (i) {
+        case 0: __builtin_amdgcn_s_waitcnt(vm_enc(C > 0 ? C : 0)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(vm_enc(C - 2 > 0 ? C - 2 : 0)); break;
+        case 2: __builtin_amdgcn_s_waitcnt(vm_enc(C - 4 > 0 ? C - 4 : 0)); break;
+        case 3: __builtin_amdgcn_s_waitcnt(vm_enc(C - 6 > 0 ? C - 6 : 0)); break;
+        default: __builtin_amdgcn_s_waitcnt(vm_enc(0)); break;
+    }
+}
+
 /* A block holds TB consecutive 8-row tiles and W = TB * SK waves: wave w works on tile w / SK and
  * takes the group pairs (w % SK) + SK * i of it; half-wave h of a step takes group 2 * pair + h.
  * The activation loads are issued first, then every weight and scale load of the wave, so one
@@ -722,23 +736,14 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
     uint4 *slice = smem4 + wave * NP * STRIDE;
     float *red = reinterpret_cast<float *>(smem4 + SK * NP * STRIDE);
 
-    /* 1. the zero areas, the activation of every pair of the wave into its slices, then the
-     * weight pieces and scales (a pair past K reads zeros everywhere) */
+    /* 1. the zero areas, the scales, then pair by pair the weight piece and the pair's activation
+     * into its slice (a pair past K reads zeros everywhere); each pair waits below for its own
+     * slice only, so its MFMAs start while the later pairs' loads are in flight */
     if (M == 2) {
 #pragma unroll
         for (int i = 0; i < NP; ++i) reinterpret_cast<uint32_t *>(slice + i * STRIDE + 64)[lane] = 0u;
     }
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)K * 2 * M);
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const int c = (wave + i * SK) * 512 + (lane & 31) * 16; /* byte of k within a row */
-        const uint32_t off = c >= K * 2 ? kOob
-                             : lane < 32 ? (uint32_t)c
-                             : M == 2    ? (uint32_t)(K * 2 + c)
-                                         : kOob;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            xr, (__attribute__((address_space(3))) void *)(slice + i * STRIDE), 16, off, 0, 0, 0);
-    }
     const size_t tile_bytes = (size_t)G * 512;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wt + (size_t)tile * tile_bytes, (uint32_t)tile_bytes);
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(st + (size_t)tile * G * 8, (uint32_t)G * 16);
@@ -752,11 +757,22 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-        const int g = 2 * (wave + i * SK) + a;
-        buf[i] = buf_load16_stream(wr, (uint32_t)(g * 512 + (kb * 8 + r) * 16));
+        {
+            const int g = 2 * (wave + i * SK) + a;
+            buf[i] = buf_load16_stream(wr, (uint32_t)(g * 512 + (kb * 8 + r) * 16));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        {
+            const int c = (wave + i * SK) * 512 + (lane & 31) * 16;
+            const uint32_t off = c >= K * 2 ? kOob
+                                 : lane < 32 ? (uint32_t)c
+                                 : M == 2    ? (uint32_t)(K * 2 + c)
+                                             : kOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void *)(slice + i * STRIDE), 16, off, 0, 0, 0);
+        }
         __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_s_waitcnt(kVmcntWeights<NP>); /* the activation, loaded first, has landed */
 
     /* 2. A chunks: 32 t + 16 a + 4 s + kb of a slice is row t's k block kb of slice s of group
      * 2p + a; ZERO + kb reads zeros. cmain: row 8a + 4t (plus 4 s a dword); coff: row
@@ -770,6 +786,8 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
         if (wave + i * SK < P) { /* wave-uniform */
+            /* the slice of pair i has landed: 2 (NP - 1 - i) loads were issued after it */
+            wait_vm<2 * (NP - 1)>(i);
             const uint4 *sl = slice + i * STRIDE;
             f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
             d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, sl[coff]),
@@ -782,8 +800,7 @@ __global__ __launch_bounds__(SK * 64) void gemv_mfma1_kernel(
             acc = fmaf((d[0] + d[1]) + (d[2] + d[3]), bf16_widen(sbits[i]), acc);
         } else {
             /* a use on this path too, so the compiler keeps the pair's loads ahead of the branch
-             * (sunk into it, they would be issued after the wait above, which then no longer
-             * covers the activation) */
+             * (sunk into it, they would no longer sit where the waits above count them) */
             asm volatile("" ::"v"(buf[i].x), "v"(sbits[i]));
         }
     }
