@@ -250,8 +250,8 @@ constexpr uint32_t kOob = 0x80000000u; /* an offset no buffer here reaches: read
  * are computed, each fixed in place by a scheduling barrier, with a use of the loads on the
  * skipped path of a pair's branch so that none is sunk into the branch. Left to itself the
  * compiler issued the scales after all the weights, and the first pair's scale FMA then waited
- * for the whole weight stream of the wave (C1 11.50 -> 11.35 us, C0 4.31 -> 4.20 with the
- * scales first; outputs bit-identical). */
+ * for the whole weight stream of the wave (with the scales first C4 16.26 -> 15.88 us, C0 4.26 ->
+ * 4.19, C1 within the noise; outputs bit-identical). */
 
 /* u / d for 0 <= u < 69905 and 1 <= d <= 16 as (u * ceil(2^20 / d)) >> 20: exact in that range
  * (the rounding excess of the multiplier, at most 15 / 2^20 per unit of u, stays below 1 / d),
@@ -1755,16 +1755,16 @@ int launch_xwave(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *o
      * pairs (C1's down) thirteen waves only tie sixteen. */
     if (pairs > 32 && pairs <= 36)
         return launch_xwave_np<OUT_F32, 3, 12, 1>(x, w, s, out, N, K, stream, residual, sub);
-    /* 17 to 20 pairs (C5, K = 5120): the matrix-core form, ten waves of two pairs, 4.02 us
-     * against 4.09-4.10 for the v_dot2 kernel of the same shape (matrix-core 7 x 3: 4.16, 5 x 4:
+    /* 17 to 20 pairs (C5, K = 5120): the matrix-core form, ten waves of two pairs, 3.97 us
+     * against 4.08 for the v_dot2 kernel of the same shape (matrix-core 7 x 3: 4.16, 5 x 4:
      * 4.27; the v_dot2 kernel: 16 waves of which twelve held one pair 4.21, 3 x 7 4.17, 4 x 5
      * 4.35, 5 x 4 4.43; interleaved runs, one box) */
     if (pairs > 16 && pairs <= 20)
         return launch_mfma1<OUT_F32, 10, 2>(x, w, s, out, N, K, stream, residual, sub);
     /* 37 to 48 pairs (C1's down, K = 9728): the matrix-core form, C1 11.45 against 11.59-11.70
      * us for the v_dot2 kernel of the same shape; thirteen waves of three pairs up to 39 pairs
-     * (11.31-11.36 against 11.37-11.44 for sixteen, 10 x 4: 11.54-11.58; three interleaved runs,
-     * one box), sixteen beyond. At 34 and 68 pairs (C4, C2) the two forms tie. */
+     * (11.35-11.45 against 11.42-11.46 for sixteen, 10 x 4: 11.54-11.58; interleaved runs, one
+     * box), sixteen beyond. At 34 and 68 pairs (C4, C2) the two forms tie. */
     if (pairs > 36 && pairs <= 39)
         return launch_mfma1<OUT_F32, 13, 3>(x, w, s, out, N, K, stream, residual, sub);
     if (pairs > 39 && pairs <= 48)
