@@ -1035,11 +1035,11 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void mfma_gemm_kernel(
  * of one ds_read_b128 pass (one k block, rows 8a + m) hit 16 distinct 16-byte bank slots.
  * Chunks of a group past K are loaded as zeros.
  * ---------------------------------------------------------------------------------------- */
-template <bool PAIR, bool OUT_F32, int TB, int SK, int NL, int MI, bool NORM = false>
+template <bool PAIR, bool OUT_F32, int TB, int SK, int NL, int MI>
 __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
     const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
-    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K,
-    const uint16_t *__restrict__ norm_w, float norm_bias, float eps, uint16_t *residual, int cm) {
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K, uint16_t *residual,
+    int cm) {
     constexpr int W = TB * SK;
     extern __shared__ uint4 smem4[];
     const int G = K >> 7;
@@ -1049,8 +1049,6 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
     const int nlds = P * 32 * M;        /* staged chunks (both groups of every pair) */
     const int nins = (nlds + 63) >> 6;  /* 1 KiB load instructions */
     float *red = reinterpret_cast<float *>(smem4 + nins * 64); /* [W][8 rows][8 tile rows] */
-    uint4 *wl = reinterpret_cast<uint4 *>(red + W * 64);       /* NORM: the norm weight [K] */
-    float *rms = reinterpret_cast<float *>(wl + (NORM ? ((K >> 3) + 63) / 64 * 64 : 0));
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1085,16 +1083,6 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
             xr, (__attribute__((address_space(3))) void *)(smem4 + j * 64), 16, off, 0, 0, 0);
         ++xloads;
     }
-    if (NORM) { /* the norm weight, [K] in order, the same way */
-        const __amdgpu_buffer_rsrc_t nr = make_rsrc(norm_w, (uint32_t)K * 2);
-        for (int j = wave; j < ((K >> 3) + 63) / 64; j += W) {
-            const int c = j * 64 + lane;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                nr, (__attribute__((address_space(3))) void *)(wl + j * 64), 16,
-                c < (K >> 3) ? (uint32_t)c * 16 : kOob, 0, 0, 0);
-        }
-    }
-
     /* 2. every weight piece and scale of this wave */
     const bool tile_ok = tile < tiles;
     const size_t tile_bytes = (size_t)G * 512;
@@ -1118,58 +1106,6 @@ __global__ __launch_bounds__(TB * SK * 64) void gemv_rows_kernel(
     (void)xloads;
     __builtin_amdgcn_s_waitcnt(kVmcntWeights<NL>);
     __syncthreads();
-
-    /* 3b. NORM: each staged row becomes its RMSNorm, BF16(x * rsqrt(sum x^2 / K + eps) *
-     * (norm_bias + w)) in the FP32 order of the reference's norm (FlashInfer RMSNorm /
-     * GemmaRMSNorm behind csrc/kernels/flashinfer_norm.cu:22-76). Wave m sums row m's squares
-     * (W >= M for every launch with NORM), then every thread normalises its staged chunks in
-     * place. The weight loads issued above keep streaming meanwhile. */
-    if (NORM) {
-        if (wave < M) {
-            /* the sum of squares in FP64 (each square of a BF16 value is exact there, and the
-             * sum of up to 2^20 of them rounds far below FP32's step), the scale formed in FP64
-             * and rounded once to FP32: the correctly rounded scale whatever the summation
-             * order, so this prologue and the FP64 restatement of the norm agree exactly */
-            double ss = 0.0;
-            for (int j = lane; j < P * 32; j += 64) { /* row m's chunks: (pair, a, slot) */
-                const int pp = j >> 5, aa = (j >> 4) & 1;
-                const uint4 ch = smem4[((pp * M + wave) * 2 + aa) * 16 + (j & 15)];
-                const uint32_t w4[4] = {ch.x, ch.y, ch.z, ch.w};
-#pragma unroll
-                for (int q2 = 0; q2 < 4; ++q2) {
-                    const double lo = bf16_widen((uint16_t)(w4[q2] & 0xFFFFu));
-                    const double hi = bf16_widen((uint16_t)(w4[q2] >> 16));
-                    ss = fma(lo, lo, ss);
-                    ss = fma(hi, hi, ss);
-                }
-            }
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
-            if (lane == 0) rms[wave] = (float)(1.0 / sqrt(ss / (double)K + (double)eps));
-        }
-        __syncthreads();
-        for (int pos = tid; pos < nlds; pos += W * 64) {
-            int m, g, c;
-            staged(pos, m, g, c);
-            if (g >= G) continue; /* a staged group past K is zero and stays zero */
-            const float rm = rms[m];
-            const uint4 v = smem4[pos];
-            const uint4 wv = wl[g * 16 + c];
-            uint32_t x4[4] = {v.x, v.y, v.z, v.w};
-            const uint32_t n4[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-            for (int q2 = 0; q2 < 4; ++q2) {
-                const float lo = bf16_widen((uint16_t)(x4[q2] & 0xFFFFu)) * rm *
-                                 (norm_bias + bf16_widen((uint16_t)(n4[q2] & 0xFFFFu)));
-                const float hi = bf16_widen((uint16_t)(x4[q2] >> 16)) * rm *
-                                 (norm_bias + bf16_widen((uint16_t)(n4[q2] >> 16)));
-                const bf16x2_t packed = {(__bf16)lo, (__bf16)hi};
-                x4[q2] = __builtin_bit_cast(uint32_t, packed);
-            }
-            smem4[pos] = make_uint4(x4[0], x4[1], x4[2], x4[3]);
-        }
-        __syncthreads();
-    }
 
     /* 4. eight MFMAs a pair. A piece past the tile's groups has scale 0 (its loads read 0) and
      * its staged activation is zero, so it adds exactly 0 without a branch; lanes of A rows
@@ -1833,37 +1769,26 @@ int launch_gemv(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *ou
 
 /* Few-row kernel: LDS for both groups of every pair of the M rows (whole 1 KiB load
  * instructions) and the wave reduction. */
-size_t rows_smem(int M, int K, int waves, bool norm = false) {
+size_t rows_smem(int M, int K, int waves) {
     const int P = (K / 128 + 1) / 2;
-    return (size_t)((P * 32 * M + 63) / 64) * 1024 + (size_t)waves * 256 +
-           (norm ? (size_t)((K / 8 + 63) / 64) * 1024 + 32 : 0);
+    return (size_t)((P * 32 * M + 63) / 64) * 1024 + (size_t)waves * 256;
 }
 
 template <bool PAIR, bool OUT_F32, int TB, int SK, int NL>
 int launch_rows_mi(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
-                   int N, int K, hipStream_t stream, const NormArgs *norm = nullptr,
-                   uint16_t *residual = nullptr, int cm = 0) {
+                   int N, int K, hipStream_t stream, uint16_t *residual = nullptr, int cm = 0) {
     if (SK * NL < (K / 128 + 1) / 2)
         return set_error(W4A16_ERR_CONFIG, "internal: a %d x %d few-row shape covers %d of %d group pairs",
                          SK, NL, SK * NL, (K / 128 + 1) / 2);
-    const size_t smem = rows_smem(M, K, TB * SK, norm != nullptr);
+    const size_t smem = rows_smem(M, K, TB * SK);
     if (smem > kMaxLds) return 1;
-    if (norm && TB * SK < M) return 1; /* the prologue gives each row a wave */
     const dim3 grid((N / 8 + TB - 1) / TB), block(TB * SK * 64);
-    const uint16_t *nw = norm ? norm->w : nullptr;
-    const float nb = norm ? norm->bias : 0.0f, ne = norm ? norm->eps : 0.0f;
-    if (M == 2 && norm)
-        hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 2, true>), grid, block,
-                           smem, stream, x, M, w, s, out, N, K, nw, nb, ne, residual, cm);
-    else if (M == 2)
+    if (M == 2)
         hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 2>), grid, block, smem,
-                           stream, x, M, w, s, out, N, K, nw, nb, ne, residual, cm);
-    else if (norm)
-        hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 4, true>), grid, block,
-                           smem, stream, x, M, w, s, out, N, K, nw, nb, ne, residual, cm);
+                           stream, x, M, w, s, out, N, K, residual, cm);
     else
         hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 4>), grid, block, smem,
-                           stream, x, M, w, s, out, N, K, nw, nb, ne, residual, cm);
+                           stream, x, M, w, s, out, N, K, residual, cm);
     return hip_status(hipGetLastError(), "gemv rows launch");
 }
 
@@ -1940,16 +1865,15 @@ int launch_rows16(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s,
 
 template <bool PAIR, bool OUT_F32>
 int launch_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
-                int K, hipStream_t stream, const NormArgs *norm = nullptr,
-                uint16_t *residual = nullptr, int cm = 0) {
+                int K, hipStream_t stream, uint16_t *residual = nullptr, int cm = 0) {
     /* long K (the staged rows would not fit LDS): registers-fed A from M = 8 (9 with the
      * residual epilogue) to 15; at 16 the split-K MFMA form is faster. C1 down, medians of
      * interleaved whole-call runs, split-K or LDS-staged against rows16x: M = 8 20.5 / 19.9 us,
      * 10 22.7 / 21.0, 13 23.9 / 22.6, 14 24.2 / 23.4, 15 24.2 / 23.9, 16 24.4 / 24.6; at M = 8
      * plan F2 23.3 against 23.6, and M = 4 and 6 tie. */
-    if (!PAIR && !norm && M >= (residual ? 9 : 8) && M <= 15 && rows16_smem(M, K, 16) > kMaxLds)
+    if (!PAIR && M >= (residual ? 9 : 8) && M <= 15 && rows16_smem(M, K, 16) > kMaxLds)
         return launch_rows16x<OUT_F32>(x, M, w, s, out, N, K, stream, residual);
-    if (M > 8 && M <= 16 && !norm && !residual)
+    if (M > 8 && M <= 16 && !residual)
         return launch_rows16<PAIR, OUT_F32>(x, M, w, s, out, N, K, stream, cm);
     if (M < 2 || M > 8) return 1;
     const int pairs = (K / 128 + 1) / 2;
@@ -1958,28 +1882,28 @@ int launch_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, v
      * C1 FFN call at M = 2: 12.58-12.66 us against 13.70-13.99 on this kernel's few-row form
      * (down alone 12.82-12.90, gate/up alone 13.55; gate/up as five waves of two ties; down as
      * thirteen of three 12.58 with the gate/up; interleaved runs, one box). */
-    if (M == 2 && !norm && !cm) {
+    if (M == 2 && !cm) {
         if (PAIR && pairs > 6 && pairs <= 12)
             return launch_mfma1<OUT_F32, 4, 3, true, 2>(x, w, s, out, N, K, stream);
         if (!PAIR && pairs > 36 && pairs <= 48)
             return launch_mfma1<OUT_F32, 16, 3, false, 2>(x, w, s, out, N, K, stream, residual);
     }
     if (pairs <= 12 && M <= 4) {
-        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 4, 1, 3>(x, M, w, s, out, N, K, stream, norm, residual, cm);
-        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 3>(x, M, w, s, out, N, K, stream, norm, residual, cm);
-        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 5>(x, M, w, s, out, N, K, stream, norm, residual, cm);
-        return launch_rows_mi<PAIR, OUT_F32, 2, 2, 6>(x, M, w, s, out, N, K, stream, norm, residual, cm);
+        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 4, 1, 3>(x, M, w, s, out, N, K, stream, residual, cm);
+        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 3>(x, M, w, s, out, N, K, stream, residual, cm);
+        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 2, 2, 5>(x, M, w, s, out, N, K, stream, residual, cm);
+        return launch_rows_mi<PAIR, OUT_F32, 2, 2, 6>(x, M, w, s, out, N, K, stream, residual, cm);
     }
     if (pairs <= 12) {
-        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 8, 1, 3>(x, M, w, s, out, N, K, stream, norm, residual, cm);
-        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 3>(x, M, w, s, out, N, K, stream, norm, residual, cm);
-        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 5>(x, M, w, s, out, N, K, stream, norm, residual, cm);
-        return launch_rows_mi<PAIR, OUT_F32, 4, 2, 6>(x, M, w, s, out, N, K, stream, norm, residual, cm);
+        if (pairs <= 3) return launch_rows_mi<PAIR, OUT_F32, 8, 1, 3>(x, M, w, s, out, N, K, stream, residual, cm);
+        if (pairs <= 6) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 3>(x, M, w, s, out, N, K, stream, residual, cm);
+        if (pairs <= 10) return launch_rows_mi<PAIR, OUT_F32, 4, 2, 5>(x, M, w, s, out, N, K, stream, residual, cm);
+        return launch_rows_mi<PAIR, OUT_F32, 4, 2, 6>(x, M, w, s, out, N, K, stream, residual, cm);
     }
-    if (pairs <= 20) return launch_rows_mi<PAIR, OUT_F32, 2, 4, 5>(x, M, w, s, out, N, K, stream, norm, residual, cm);
-    if (pairs <= 40) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 5>(x, M, w, s, out, N, K, stream, norm, residual, cm);
-    if (pairs <= 48) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 6>(x, M, w, s, out, N, K, stream, norm, residual, cm);
-    if (pairs <= 80) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 10>(x, M, w, s, out, N, K, stream, norm, residual, cm);
+    if (pairs <= 20) return launch_rows_mi<PAIR, OUT_F32, 2, 4, 5>(x, M, w, s, out, N, K, stream, residual, cm);
+    if (pairs <= 40) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 5>(x, M, w, s, out, N, K, stream, residual, cm);
+    if (pairs <= 48) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 6>(x, M, w, s, out, N, K, stream, residual, cm);
+    if (pairs <= 80) return launch_rows_mi<PAIR, OUT_F32, 2, 8, 10>(x, M, w, s, out, N, K, stream, residual, cm);
     return 1;
 }
 
@@ -2264,7 +2188,7 @@ static int run_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *
          * (then the MFMA form with one live row) */
         const bool gemv = rows == 1 && (!PAIR || K <= kMaxGemvK);
         int st = gemv ? launch_gemv<PAIR, F32>(xs, w, s, os, N, K, stream)
-                      : launch_rows<PAIR, F32>(xs, rows, w, s, os, N, K, stream, nullptr, nullptr, cm);
+                      : launch_rows<PAIR, F32>(xs, rows, w, s, os, N, K, stream, nullptr, cm);
         if (st > 0) st = launch_mfma<OUT>(xs, rows, w, s, os, N, K, stream, nullptr, cm);
         if (st) return st;
     }
@@ -2443,16 +2367,13 @@ static int mlp_norm_common(const uint16_t *residual, const uint16_t *norm_w, int
     uint16_t *normed = ws;                          /* [M, hidden] (M > 1) */
     uint16_t *act = ws + (size_t)M * hidden;        /* [M, inter] */
     /* The prologue costs every gate/up block a normalisation of the whole row, so it pays only
-     * while a block's waves each hold all of K (measured at H = 2560: 16.2 us per norm + FFN
-     * call fused, 17.8 us with a separate norm launch); at H = 5120 the separate launch is
-     * cheaper (35.0 against 38.4 us). */
+     * while a block's waves each hold all of K, at one row (C1 norm + FFN 12.8 us fused against
+     * 13.7 with a separate norm launch; at H = 5120 the separate launch is cheaper, 35.0 against
+     * 38.4 us). At M = 2 the separate norm, then the two-row matrix-core kernels, beats the
+     * few-row kernel's own prologue: C1 14.6-14.7 against 15.6-15.8 us, C2 38.3 against 42.8. */
     st = 1;
     if (M == 1 && (hidden / W4A16_GROUP + 1) / 2 <= kMaxLoads)
         st = launch_gemv<true, false>(residual, gup, gus, act, 2 * inter, hidden, s, &na);
-    else if (M == 2) /* the few-row kernel's own prologue (C3 norm + FFN: M = 2 18.1-18.4 us
-                      * against 19.2 with the separate norm; M = 4 21.5 against 20.4-20.9 and
-                      * M = 8 26.2-26.7 against 24.0, every block normalising all M rows) */
-        st = launch_rows<true, false>(residual, M, gup, gus, act, 2 * inter, hidden, s, &na);
     const bool cm = st > 0 && chunk_major_down(M, inter);
     if (st > 0) {
         st = launch_rmsnorm(normed, residual, norm_w, hidden, M, na.bias, eps, s);
@@ -2548,7 +2469,7 @@ extern "C" int mlp_int4_residual_norm_bf16(uint16_t *residual, const uint16_t *s
         if (st <= 0) return st;
     }
     if (M >= 2 && M <= 16) { /* the few-row or MFMA down kernel adds into the residual */
-        st = launch_rows<false, false>(act, M, dnp, dns, out, hidden, inter, s, nullptr, residual);
+        st = launch_rows<false, false>(act, M, dnp, dns, out, hidden, inter, s, residual);
         if (st > 0) st = launch_mfma<kOutBf16>(act, M, dnp, dns, out, hidden, inter, s, residual);
         return st;
     }

@@ -170,9 +170,9 @@ int w4a16_rmsnorm_bf16(uint16_t *out, const uint16_t *x, const uint16_t *weight,
                        int rows, int norm_style, float eps, void *stream);
 
 /* forward_mlp (reference csrc/kernels/layers.cu:150-159): the post-attention RMSNorm of the
- * residual [M, hidden], then the INT4 MLP. At M = 1 and M = 2 the norm is formed inside the
- * gate/up kernel's activation staging (no separate launch, no normed round trip; the normed
- * part of ws is then left unwritten); other M normalise into ws first. ws: M * (hidden +
+ * residual [M, hidden], then the INT4 MLP. At M = 1 (hidden up to 3072) the norm is formed
+ * inside the gate/up kernel's activation staging (no separate launch, no normed round trip;
+ * the normed part of ws is then left unwritten); other M normalise into ws first. ws: M * (hidden +
  * intermediate) BF16 (normed, then act in the order mlp_int4_bf16 gives it). The norm's scale is rounded once to FP32 from an FP64
  * sum of squares; the products are FlashInfer's FP32 ones in its order. */
 int mlp_int4_norm_bf16(const uint16_t *residual, const uint16_t *norm_w, int norm_style,

@@ -415,10 +415,10 @@ def test_rmsnorm_parity(cuda, style):
 @pytest.mark.parametrize("m", [1, 2, 16])
 def test_ffn_norm_parity(cuda, style, m):
     """mlp_int4_norm (forward_mlp, reference csrc/kernels/layers.cu:150-159) against the
-    oracle's RMSNorm followed by the oracle FFN, at the end-to-end bar of test_ffn_parity; up to
-    M = 8 the norm runs inside the gate/up kernel (the GEMV's or the few-row kernel's prologue),
-    at M = 16 in its own kernel ahead of the MFMA kernels. The FP32 partial form is checked
-    against the oracle's unrounded partial."""
+    oracle's RMSNorm followed by the oracle FFN, at the end-to-end bar of test_ffn_parity; at
+    M = 1 the norm runs inside the gate/up kernel (the block-staged GEMV's prologue), otherwise in
+    its own kernel ahead of the FFN. The FP32 partial form is checked against the oracle's
+    unrounded partial."""
     hidden, inter = 2560, 9728
     say(f"ffn norm style={style} M={m}")
     gup, gus, dp, ds = make_ffn(hidden, inter)
@@ -443,14 +443,11 @@ def test_ffn_norm_parity(cuda, style, m):
 
 @pytest.mark.parametrize("m", [2, 3, 5, 8])
 def test_ffn_norm_fused_rows(cuda, m):
-    """mlp_int4_norm for 2 <= M <= 8 against the explicit composition, for both norm styles: at
-    M = 2 the few-row kernel's own prologue, whose FP64 sum of squares gives the correctly
-    rounded scale, against the oracle's RMSNorm (FP64 scale, FP32 products) followed by the
-    fused gate/up (another kernel at M = 2, the matrix-core GEMV: act to the parity bar, then
-    the down projection bit-identical on the fused call's own act); from M = 3 the standalone
-    RMSNorm then the fused gate/up, act and output bit-identical. Within rel-L2 1e-3 of the oracle end to end. (Against the oracle's per-element bar
-    these residual inputs leave a few act values at 3 BF16 ULP at M = 5 and 8: one normalised
-    value rounded the other way by the FP32 norm moves every gate/up sum.)"""
+    """mlp_int4_norm for 2 <= M <= 8 against the explicit composition, for both norm styles: the
+    standalone RMSNorm then the fused gate/up, act and output bit-identical (the same kernels as
+    the call's), and within rel-L2 1e-3 of the oracle end to end. (Against the oracle's
+    per-element bar these residual inputs leave a few act values at 3 BF16 ULP at M = 5 and 8:
+    one normalised value rounded the other way moves every gate/up sum.)"""
     import torch
 
     hidden, inter = 2560, 9728
@@ -464,16 +461,9 @@ def test_ffn_norm_fused_rows(cuda, m):
         ws = torch.empty((m, hidden + inter), dtype=xd.dtype, device=cuda)
         out = from_dev(w4a16.mlp_int4_norm(xd, wd, style, 1e-6, gu, dn, ws=ws))
         act = ws_act(from_dev(ws.reshape(-1)[m * hidden:]), m, inter)
-        if m == 2:  # the prologue's scale is the correctly rounded one, as the oracle's
-            normed = to_dev(oracle.rmsnorm_bf16(x, w, style, 1e-6), cuda)
-        else:
-            normed = w4a16.rmsnorm(xd, wd, style, 1e-6)
+        normed = w4a16.rmsnorm(xd, wd, style, 1e-6)
         act2 = w4a16.gate_up_silu(normed, gu)
-        if m == 2:  # the prologue's few-row kernel against the matrix-core gate/up of M = 2
-            assert_parity(act, from_dev(act2), f"norm gate/up M={m} against its two stages")
-            act2 = to_dev(act, cuda)  # the down kernel checked on the fused call's own act
-        else:
-            assert np.array_equal(act, from_dev(act2)), (m, style)
+        assert np.array_equal(act, from_dev(act2)), (m, style)
         down2 = from_dev(w4a16.gemm_int4_bf16(act2, dn))
         if m < 4 or m >= 8:  # the same down kernel and summation order
             assert np.array_equal(out, down2), (m, style)
