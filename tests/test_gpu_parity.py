@@ -111,9 +111,9 @@ def test_quantize_device_bit_exact(cuda):
                                  # two pairs (7-10) and four of three (11-12) a tile, including
                                  # odd group counts
                                  (64, 1792), (64, 2816), (40, 3072), (16, 2944), (56, 1920),
-                                 # 37 to 48 pairs: the matrix-core kernel, sixteen waves of
-                                 # three pairs (75 groups is odd)
-                                 (64, 9472), (48, 9600), (32, 12288),
+                                 # 37 to 48 pairs: the matrix-core kernel, thirteen waves of
+                                 # three pairs to 39, sixteen beyond (75 and 79 groups are odd)
+                                 (64, 9472), (48, 9600), (32, 12288), (24, 10112), (40, 9984),
                                  # 33 to 36 pairs: twelve waves of three pairs a tile
                                  (512, 8448 + 128), (128, 8704), (64, 9216),
                                  # 17 to 20 pairs: ten waves of two pairs a tile (the
@@ -167,8 +167,9 @@ def test_few_rows_parity(cuda, m):
         act = from_dev(w4a16.gate_up_silu(to_dev(x, cuda), gu))
         mid = oracle.gemm_bf16(x, gp, gs, 2 * inter, hidden)
         assert_parity(act, oracle.silu_mul_packed(mid, m, inter), f"gate/up M={m} H={hidden}")
-    if m == 2:
-        n, k = 48, 9600  # 75 groups: the last pair's second group past K
+    # two rows on the matrix-core GEMV's long-K form at odd group counts (75 groups: 38 pairs;
+    # 79 groups: 40 pairs, sixteen waves), the last pair's second group past K
+    for n, k in ([(48, 9600), (24, 10112)] if m == 2 else []):
         say(f"gemm M={m} n={n} k={k}")
         p, s = make_weight(n, k, seed=n + k + m)
         x = oracle.synth_activation(m, k, seed=200 + m)
