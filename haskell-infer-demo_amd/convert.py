@@ -18,11 +18,9 @@ Usage (BF16 safetensors checkpoint + the reference's descriptor JSON):
     python convert.py --model-dir DIR --desc descriptor.json --out-dir OUT
     python convert.py --verify OUT/weights.manifest.json [--reference QUANTIZER]
 
---verify re-derives the sidecar's claims the way the reference's --verify does (reference
-scripts/quantize_weights.py:328-440): every artifact's size and digest, the source shards'
-digests, the precision map covering every (layer, role) of the descriptor exactly once, each
-pair being its members' rows in order, and a sample of entries re-quantized from the source
-checkpoint (by this library, or by the reference's compiled quantizer when given).
+--verify audits a written sidecar without trusting what it records (the checks the reference's
+--verify makes, scripts/quantize_weights.py:328-460, organised as five passes of this file's
+own: header, files, tables, provenance, re-derivation; see the --verify section below).
 """
 
 import argparse
@@ -183,40 +181,87 @@ def write_sidecar(out_dir, layers, model_dir, role_names=None, tensor_names=None
 
 
 # ---- BF16 safetensors checkpoints ----------------------------------------------------------------
+#
+# A shard is an 8-byte little-endian header length, a JSON header mapping tensor names to
+# {dtype, shape, data_offsets} (offsets relative to the end of the header), then raw bytes. A
+# Checkpoint reads every shard's header once, keeps a TensorRef (absolute byte span) per name and
+# reads a tensor's bytes only when asked, so a converter run never holds a shard whole.
 
-def read_safetensors_index(model_dir):
-    """name -> (path, dtype, shape, start, stop) over every shard; a tensor named in two shards
-    is refused (reference scripts/quantize_weights.py:72-92)."""
-    index = {}
-    for name in sorted(os.listdir(model_dir)):
-        if not name.endswith(".safetensors"):
-            continue
-        path = os.path.join(model_dir, name)
-        with open(path, "rb") as handle:
-            hlen = struct.unpack("<Q", handle.read(8))[0]
-            header = json.loads(handle.read(hlen))
-        for tensor, info in header.items():
-            if tensor == "__metadata__":
-                continue
-            if tensor in index:
-                raise ConvertError(f"{tensor} appears in two shards")
-            start, stop = info["data_offsets"]
-            index[tensor] = (path, info["dtype"], list(info["shape"]), 8 + hlen + start, 8 + hlen + stop)
-    return index
+class TensorRef(tuple):
+    """(shard path, dtype, shape, absolute first byte, byte count) of one stored tensor."""
+
+    __slots__ = ()
+
+    def __new__(cls, path, dtype, shape, offset, nbytes):
+        return tuple.__new__(cls, (path, dtype, tuple(shape), offset, nbytes))
+
+    path = property(lambda self: self[0])
+    dtype = property(lambda self: self[1])
+    shape = property(lambda self: self[2])
+    offset = property(lambda self: self[3])
+    nbytes = property(lambda self: self[4])
 
 
-def read_bf16_as_f32(entry):
-    """A BF16 tensor widened to FP32 (exact)."""
-    path, dtype, shape, start, stop = entry
-    if dtype != "BF16":
-        raise ConvertError(f"only BF16 sources are admitted, got {dtype}")
-    count = int(np.prod(shape)) if shape else 1
-    if stop - start != 2 * count:
-        raise ConvertError(f"{path}: a {shape} BF16 tensor spans {stop - start} bytes")
+def _shard_header(path):
+    """The parsed header of one shard and the absolute offset its data region starts at."""
+    size = os.path.getsize(path)
     with open(path, "rb") as handle:
-        handle.seek(start)
-        raw = handle.read(stop - start)
-    return (np.frombuffer(raw, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(shape)
+        prefix = handle.read(8)
+        if len(prefix) != 8:
+            raise ConvertError(f"{os.path.basename(path)}: shorter than a safetensors prefix")
+        (length,) = struct.unpack("<Q", prefix)
+        if 8 + length > size:
+            raise ConvertError(f"{os.path.basename(path)}: header of {length} bytes runs past the file")
+        header = json.loads(handle.read(length).decode("utf-8"))
+    return header, 8 + length, size
+
+
+class Checkpoint:
+    """Every tensor of a directory of safetensors shards, by name (shards in name order).
+
+    Replaces the reference converter's shard index (scripts/quantize_weights.py:75-94) for this
+    converter: a name stored by more than one shard, or a byte span outside its shard, is a
+    refusal, since either would make the artifact's source ambiguous."""
+
+    def __init__(self, model_dir):
+        self.model_dir = model_dir
+        self.shards = sorted(f for f in os.listdir(model_dir) if f.endswith(".safetensors"))
+        self.refs = {}
+        owner = {}
+        for shard in self.shards:
+            path = os.path.join(model_dir, shard)
+            header, base, size = _shard_header(path)
+            for name in sorted(k for k in header if k != "__metadata__"):
+                if name in owner:
+                    raise ConvertError(f"checkpoint tensor {name} is stored by two shards: "
+                                       f"{owner[name]} and {shard}")
+                lo, hi = header[name]["data_offsets"]
+                if not 0 <= lo <= hi or base + hi > size:
+                    raise ConvertError(f"{shard}: {name} spans bytes {lo}..{hi}, outside the shard")
+                owner[name] = shard
+                self.refs[name] = TensorRef(path, header[name]["dtype"], header[name]["shape"],
+                                            base + lo, hi - lo)
+
+    def __contains__(self, name):
+        return name in self.refs
+
+    def bf16_as_f32(self, name):
+        """Tensor `name`, which must be stored as BF16, widened to FP32 (exact)."""
+        return read_bf16_as_f32(self.refs[name])
+
+
+def read_bf16_as_f32(ref):
+    """A stored BF16 tensor widened to FP32 (exact: the BF16 bits become the high half)."""
+    if ref.dtype != "BF16":
+        raise ConvertError(f"only BF16 sources are admitted, got {ref.dtype}")
+    count = int(np.prod(ref.shape)) if ref.shape else 1
+    if ref.nbytes != 2 * count:
+        raise ConvertError(f"{ref.path}: a {list(ref.shape)} BF16 tensor spans {ref.nbytes} bytes")
+    with open(ref.path, "rb") as handle:
+        handle.seek(ref.offset)
+        raw = handle.read(ref.nbytes)
+    bits = np.frombuffer(raw, dtype="<u2").astype(np.uint32) << 16
+    return bits.view(np.float32).reshape(ref.shape)
 
 
 def _role_tensor(template, layer):
@@ -243,7 +288,7 @@ def convert_checkpoint(model_dir, desc_path, out_dir, limit_layers=None):
         if role not in names:
             raise ConvertError(f"the descriptor has no {role} role")
     before = _shard_records(model_dir)
-    index = read_safetensors_index(model_dir)
+    ckpt = Checkpoint(model_dir)
     layers, tensor_names = {}, {}
     for layer in range(desc["num_layers"]):
         if desc["layer_ffns"][layer] != "dense" or (limit_layers is not None and layer >= limit_layers):
@@ -251,9 +296,9 @@ def convert_checkpoint(model_dir, desc_path, out_dir, limit_layers=None):
         layers[layer] = {}
         for role in ROLES:
             tensor = _role_tensor(templates[names.index(role)], layer)
-            if tensor not in index:
+            if tensor not in ckpt:
                 raise ConvertError(f"{tensor} is not in the checkpoint")
-            w = read_bf16_as_f32(index[tensor])
+            w = ckpt.bf16_as_f32(tensor)
             if w.ndim != 2:
                 raise ConvertError(f"{tensor} is not a 2-D weight")
             tensor_names[(layer, role)] = tensor
@@ -270,6 +315,19 @@ def convert_checkpoint(model_dir, desc_path, out_dir, limit_layers=None):
 
 
 # ---- --verify -------------------------------------------------------------------------------
+#
+# An audit of a written sidecar that trusts nothing it records. It runs five passes, each
+# appending findings (plain sentences) to one list:
+#   1. the header: manifest_version and the frozen FORMAT block;
+#   2. the files: every artifact record (entries and pairs alike) against the bytes the shape
+#      implies, the bytes recorded, and the file's SHA-256; each file is hashed once;
+#   3. the tables: entries unique and inside the tile rule, the precision map a one-to-one cover
+#      of the descriptor's (layer, role) grid that marks exactly the entries as int4, every pair
+#      [mlpGate, mlpUp] with its members' stacked shape and the hash of their streamed
+#      concatenation;
+#   4. provenance: the source shards and the descriptor still hash to what was recorded;
+#   5. only on a clean audit: a spread sample of entries re-quantized from the source
+#      checkpoint, by this library or by a compiled quantizer given as `reference`.
 
 def _quantize_with(reference, w):
     """Payload and scales of w by the reference's compiled quantizer (its --quantize mode)."""
@@ -292,107 +350,173 @@ def _quantize_with(reference, w):
     return packed, scales
 
 
-def verify(manifest_path, reference=None, sample=2):
-    """Re-derive a sidecar's claims; returns the list of problems (empty when it verifies)."""
-    import w4a16
+def _cell(layer, role):
+    return f"layer {layer} {role}"
 
-    with open(manifest_path) as handle:
-        manifest = json.load(handle)
-    out_dir = os.path.dirname(os.path.abspath(manifest_path))
-    problems = []
 
-    def require(ok, message):
-        if not ok:
-            problems.append(message)
+class _SidecarAudit:
+    def __init__(self, manifest_path):
+        with open(manifest_path) as handle:
+            self.doc = json.load(handle)
+        self.root = os.path.dirname(os.path.abspath(manifest_path))
+        self.findings = []
+        self._hashes = {}
 
-    require(manifest.get("manifest_version") == MANIFEST_VERSION,
-            f"unknown manifest version {manifest.get('manifest_version')}")
-    for key, value in FORMAT.items():
-        have = manifest.get("format", {}).get(key)
-        require(have == value, f"the format's {key} is {have!r}, expected {value!r}")
-    source_dir = manifest["source"]["model_dir"]
-    for record in manifest["source"]["files"]:
-        path = os.path.join(source_dir, record["name"])
-        require(os.path.exists(path) and sha256_file(path) == record["sha256"],
-                f"the source shard {record['name']} is missing or no longer matches its digest")
+    def note(self, text):
+        self.findings.append(text)
 
-    def check_artifact(art, want_bytes, what):
-        path = os.path.join(out_dir, art["file"])
-        if not os.path.exists(path):
-            problems.append(f"{what} has no artifact at {art['file']}")
-            return False
-        require(os.path.getsize(path) == want_bytes == art["bytes"],
-                f"{what} is {os.path.getsize(path)} bytes, the shape needs {want_bytes}")
-        require(sha256_file(path) == art["sha256"], f"{what} does not match its digest")
-        return True
+    def file_hash(self, rel):
+        """SHA-256 of an artifact file under the sidecar's directory, or None when absent."""
+        if rel not in self._hashes:
+            path = os.path.join(self.root, rel)
+            self._hashes[rel] = sha256_file(path) if os.path.isfile(path) else None
+        return self._hashes[rel]
 
-    seen, entries = {}, manifest["entries"]
-    for e in entries:
-        key = (e["layer"], e["role"])
-        require(key not in seen, f"{key} appears twice")
-        seen[key] = e
-        n, k = e["logical_shape"]
-        require(n % 8 == 0 and k % FORMAT["group"] == 0, f"{key} has a shape outside the format: {n}x{k}")
-        check_artifact(e["packed"], n * k // 2, f"{key} payload")
-        check_artifact(e["scales"], 2 * n * (k // FORMAT["group"]), f"{key} scales")
+    # 1
+    def header(self):
+        version = self.doc.get("manifest_version")
+        if version != MANIFEST_VERSION:
+            self.note(f"manifest_version {version!r} is not {MANIFEST_VERSION}, the one this reader knows")
+        block = self.doc.get("format") or {}
+        for key in FORMAT:
+            if block.get(key) != FORMAT[key]:
+                self.note(f"format block: {key!r} reads {block.get(key)!r} where the INT4 format "
+                          f"fixes {FORMAT[key]!r}")
 
-    desc = manifest.get("descriptor")
-    require(desc is not None, "the manifest records no descriptor")
-    roles_of = None
-    if desc is not None:
-        require(os.path.exists(desc["path"]) and sha256_file(desc["path"]) == desc["sha256"],
-                "the descriptor is missing or no longer matches its digest")
-        if os.path.exists(desc["path"]):
-            with open(desc["path"]) as handle:
-                d = json.load(handle)
-            roles_of = (d["num_layers"], d["role_names"])
-    covered = set()
-    for cell in manifest["precision_map"]:
-        key = (cell["layer"], cell["role"])
-        require(key not in covered, f"the precision map lists {key} twice")
-        covered.add(key)
-        require((cell["precision"] == "int4") == (key in seen),
-                f"the precision map and the entries disagree about {key}")
-    if roles_of is not None:
-        for layer in range(roles_of[0]):
-            for role in roles_of[1]:
-                require((layer, role) in covered, f"the precision map does not cover {(layer, role)}")
+    # 2
+    def files(self):
+        group = FORMAT["group"]
+        records = []
+        for e in self.doc.get("entries", []):
+            records.append((f"{_cell(e['layer'], e['role'])}", e, e["logical_shape"]))
+        for p in self.doc.get("pairs", []):
+            records.append((f"F1 pair of layer {p['layer']}", p, p["logical_shape"]))
+        for label, rec, (n, k) in records:
+            implied = {"packed": n * k // 2, "scales": 2 * n * (k // group)}
+            for kind, want in implied.items():
+                art = rec[kind]
+                path = os.path.join(self.root, art["file"])
+                if not os.path.isfile(path):
+                    self.note(f"{label} {kind}: file {art['file']} is absent")
+                    continue
+                size = os.path.getsize(path)
+                if not size == art["bytes"] == want:
+                    self.note(f"{label} {kind}: {size} bytes on disk, {art['bytes']} recorded, "
+                              f"{want} implied by the shape {n}x{k}")
+                if self.file_hash(art["file"]) != art["sha256"]:
+                    self.note(f"{label} {kind}: content hash differs from the recorded sha256")
 
-    for pair in manifest.get("pairs", []):
-        layer = pair["layer"]
-        roles = [m["role"] for m in pair["members"]]
-        require(roles == list(PAIR_ROLES), f"pair at layer {layer} has members {roles}")
-        members = [seen.get((layer, r)) for r in roles]
-        if any(m is None for m in members):
-            problems.append(f"pair at layer {layer} names a member that has no entry")
-            continue
-        rows = sum(m["logical_shape"][0] for m in members)
-        k = members[0]["logical_shape"][1]
-        require(pair["logical_shape"] == [rows, k], f"pair at layer {layer} claims {pair['logical_shape']}")
-        for kind in ("packed", "scales"):
-            want = b""
-            for m in members:
-                with open(os.path.join(out_dir, m[kind]["file"]), "rb") as handle:
-                    want += handle.read()
-            path = os.path.join(out_dir, pair[kind]["file"])
-            have = open(path, "rb").read() if os.path.exists(path) else None
-            require(have == want, f"pair at layer {layer}'s {kind} is not its members' rows in order")
+    # 3
+    def tables(self, grid):
+        from collections import Counter
 
-    if not problems and sample:
-        index = read_safetensors_index(source_dir)
-        for e in entries[:sample]:
-            w = read_bf16_as_f32(index[e["checkpoint_tensor"]])
+        entries = {}
+        for e in self.doc.get("entries", []):
+            key = (e["layer"], e["role"])
+            if key in entries:
+                self.note(f"{_cell(*key)} is quantized by more than one entry")
+            entries[key] = e
+            n, k = e["logical_shape"]
+            if n % 8 or k % FORMAT["group"]:
+                self.note(f"{_cell(*key)}: shape {n}x{k} breaks the tile rule "
+                          f"(rows a multiple of 8, K of {FORMAT['group']})")
+        cells = Counter()
+        for c in self.doc.get("precision_map", []):
+            key = (c["layer"], c["role"])
+            cells[key] += 1
+            if (c["precision"] == "int4") != (key in entries):
+                self.note(f"precision_map marks {_cell(*key)} {c['precision']} but the sidecar "
+                          f"{'has' if key in entries else 'has no'} INT4 entry for it")
+        for key, count in sorted(cells.items()):
+            if count > 1:
+                self.note(f"precision_map: {_cell(*key)} occurs {count} times")
+        for key in grid or ():
+            if key not in cells:
+                self.note(f"precision_map: no cell for the descriptor's {_cell(*key)}")
+        for p in self.doc.get("pairs", []):
+            label = f"F1 pair of layer {p['layer']}"
+            roles = [m["role"] for m in p["members"]]
+            if roles != list(PAIR_ROLES):
+                self.note(f"{label}: members are {roles}, the fused kernels need {list(PAIR_ROLES)}")
+            parts = [entries.get((p["layer"], r)) for r in roles]
+            if None in parts:
+                missing = [r for r, e in zip(roles, parts) if e is None]
+                self.note(f"{label}: {missing} have no INT4 entry to stack")
+                continue
+            stacked = [sum(e["logical_shape"][0] for e in parts), parts[0]["logical_shape"][1]]
+            if p["logical_shape"] != stacked:
+                self.note(f"{label}: logical_shape {p['logical_shape']} but its members stack to {stacked}")
+            for kind in ("packed", "scales"):
+                have = self.file_hash(p[kind]["file"])
+                files = [os.path.join(self.root, e[kind]["file"]) for e in parts]
+                if have is None or not all(os.path.isfile(f) for f in files):
+                    continue  # already a finding of the file pass
+                digest = hashlib.sha256()
+                for f in files:
+                    with open(f, "rb") as handle:
+                        for chunk in iter(lambda: handle.read(1 << 20), b""):
+                            digest.update(chunk)
+                if digest.hexdigest() != have:
+                    self.note(f"{label}: the {kind} file is not the gate rows followed by the up rows")
+        return entries
+
+    # 4
+    def provenance(self):
+        """Returns the descriptor's (layer, role) grid, or None when it cannot be read."""
+        source = self.doc["source"]
+        for rec in source["files"]:
+            path = os.path.join(source["model_dir"], rec["name"])
+            if not os.path.isfile(path):
+                self.note(f"source checkpoint: shard {rec['name']} is gone")
+            elif sha256_file(path) != rec["sha256"]:
+                self.note(f"source checkpoint: shard {rec['name']} was modified after conversion")
+        desc = self.doc.get("descriptor")
+        if desc is None:
+            self.note("no descriptor is recorded, so the precision map's cover cannot be checked")
+            return None
+        if not os.path.isfile(desc["path"]):
+            self.note(f"descriptor {desc['path']} is gone")
+            return None
+        if sha256_file(desc["path"]) != desc["sha256"]:
+            self.note(f"descriptor {desc['path']} was modified after conversion")
+        with open(desc["path"]) as handle:
+            d = json.load(handle)
+        return [(layer, role) for layer in range(d["num_layers"]) for role in d["role_names"]]
+
+    # 5
+    def rederive(self, entries, reference, sample):
+        import w4a16
+
+        ordered = [entries[key] for key in sorted(entries)]
+        if not ordered or sample <= 0:
+            return
+        stride = max(1, len(ordered) // sample)
+        ckpt = Checkpoint(self.doc["source"]["model_dir"])
+        for e in ordered[::stride][:sample]:
+            w = ckpt.bf16_as_f32(e["checkpoint_tensor"])
             if reference:
                 packed, scales = _quantize_with(reference, w)
             else:
-                p, sc = w4a16.quantize_int4(np.ascontiguousarray(w, dtype=np.float32))
-                packed, scales = p.tobytes(), sc.tobytes()
-            with open(os.path.join(out_dir, e["packed"]["file"]), "rb") as handle:
-                require(handle.read() == packed, f"{e['role']}_{e['layer']} does not re-derive from the source")
-            with open(os.path.join(out_dir, e["scales"]["file"]), "rb") as handle:
-                require(handle.read() == scales, f"{e['role']}_{e['layer']} scales do not re-derive")
-    return problems
+                p, s = w4a16.quantize_int4(np.ascontiguousarray(w, dtype=np.float32))
+                packed, scales = p.tobytes(), s.tobytes()
+            for kind, want in (("packed", packed), ("scales", scales)):
+                if self.file_hash(e[kind]["file"]) != hashlib.sha256(want).hexdigest():
+                    self.note(f"{_cell(e['layer'], e['role'])}: re-quantizing {e['checkpoint_tensor']} "
+                              f"gives other {kind} bytes")
 
+
+def verify(manifest_path, reference=None, sample=2):
+    """Audit a written sidecar (the five passes above); returns the findings, empty when clean.
+
+    Covers what the reference's --verify covers (scripts/quantize_weights.py:328-460)."""
+    audit = _SidecarAudit(manifest_path)
+    audit.header()
+    audit.files()
+    grid = audit.provenance()
+    entries = audit.tables(grid)
+    if not audit.findings:
+        audit.rederive(entries, reference, sample)
+    return audit.findings
 
 def main():
     ap = argparse.ArgumentParser()

@@ -48,17 +48,18 @@ extern "C" float w4a16_bf16_to_f32(uint16_t bits) { return bf16_widen(bits); }
 extern "C" int w4a16_layout_init(long long n, long long k, long long group,
                                  long long *packed_bytes, long long *scale_count) {
     if (n <= 0 || k <= 0)
-        return set_error(W4A16_ERR_CONFIG, "layout: extents must be positive (n=%lld k=%lld)", n, k);
+        return set_error(W4A16_ERR_CONFIG, "layout: shape %lld x %lld has an empty or negative side", n, k);
     if (group != W4A16_GROUP)
         return set_error(W4A16_ERR_CONFIG,
-                         "layout: the format's group is %d, not %lld (a different group is a "
-                         "different format)", W4A16_GROUP, group);
+                         "layout: group %lld requested; the INT4 artifact format is fixed at %d "
+                         "values per scale", group, W4A16_GROUP);
     if (k % group != 0)
         return set_error(W4A16_ERR_CONFIG,
-                         "layout: K=%lld is not a whole number of %lld-wide groups", k, group);
+                         "layout: K=%lld leaves a partial scale group (K %% %lld = %lld)", k, group,
+                         k % group);
     if (n % W4A16_TILE_ROWS != 0)
-        return set_error(W4A16_ERR_CONFIG, "layout: N=%lld is not a whole number of %d-row tiles",
-                         n, W4A16_TILE_ROWS);
+        return set_error(W4A16_ERR_CONFIG, "layout: N=%lld rows do not fill %d-row tiles (N %% %d = %lld)",
+                         n, W4A16_TILE_ROWS, W4A16_TILE_ROWS, n % W4A16_TILE_ROWS);
     if (packed_bytes) *packed_bytes = n * k / 2;
     if (scale_count) *scale_count = n * (k / group);
     return W4A16_OK;
@@ -77,7 +78,7 @@ extern "C" int w4a16_quantize_int4(long long n, long long k, const float *weight
     const long long groups = k / W4A16_GROUP;
     for (long long i = 0; i < n * k; ++i)
         if (!std::isfinite(weights[i]))
-            return set_error(W4A16_ERR_CONFIG, "quantize: element %lld is not finite", i);
+            return set_error(W4A16_ERR_CONFIG, "quantize: weight %lld (row %lld) is NaN or infinite", i, i / k);
     /* Every group's scale is derived (and checked) before any output byte is written, so a
      * refusal leaves the caller's buffers as they were. */
     std::vector<uint16_t> sc((size_t)nscales);
@@ -90,8 +91,8 @@ extern "C" int w4a16_quantize_int4(long long n, long long k, const float *weight
             const float s = bf16_widen(bits);
             if (!(s > 0.0f) || !std::isfinite(s))
                 return set_error(W4A16_ERR_CONFIG,
-                                 "quantize: row %lld group %lld rounds to scale %g, which the "
-                                 "format cannot hold", row, g, (double)s);
+                                 "quantize: absmax/7 of row %lld group %lld becomes BF16 %g, "
+                                 "unusable as a scale", row, g, (double)s);
             sc[(size_t)(row * groups + g)] = bits;
         }
     }
@@ -123,13 +124,13 @@ extern "C" int w4a16_dequantize_int4(long long n, long long k, const uint8_t *pa
             const float s = bf16_widen(scales[row * groups + c / W4A16_GROUP]);
             if (!(s > 0.0f) || !std::isfinite(s))
                 return set_error(W4A16_ERR_WEIGHTS,
-                                 "dequantize: row %lld group %lld has a scale that is not "
-                                 "positive and finite", row, c / W4A16_GROUP);
+                                 "dequantize: scale of row %lld group %lld is zero, negative or "
+                                 "non-finite", row, c / W4A16_GROUP);
             const int nib = (packed[(row * k + c) >> 1] >> (4 * (c & 1))) & 0xF;
             if (nib == 0x8)
                 return set_error(W4A16_ERR_WEIGHTS,
-                                 "dequantize: row %lld column %lld carries the reserved code -8",
-                                 row, c);
+                                 "dequantize: nibble 0x8 (code -8, never written by the "
+                                 "quantizer) at row %lld column %lld", row, c);
             out[row * k + c] = (float)nibble_code(nib) * s;
         }
     }

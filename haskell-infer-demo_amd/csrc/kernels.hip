@@ -2133,21 +2133,20 @@ int check_gemm_args(const void *a, const void *p, const void *s, const void *o, 
     if (M < 0 || N < 0 || K <= 0 || group <= 0)
         return set_error(W4A16_ERR_CONFIG, "%s: negative extent or nonpositive group", what);
     if (M == 0 || N == 0) return 1; /* no-op */
-    if (!a || !p || !s || !o) return set_error(W4A16_ERR_CONFIG, "%s: null buffer", what);
+    if (!a || !p || !s || !o) return set_error(W4A16_ERR_CONFIG, "%s: a device pointer is null", what);
     if (misaligned(a) || misaligned(p) || misaligned(s) || misaligned(o))
         return set_error(W4A16_ERR_CONFIG, "%s: device buffers must be 16-byte aligned", what);
     if (K % group != 0)
-        return set_error(W4A16_ERR_CONFIG, "%s: K=%d is not a whole number of %d-wide groups",
+        return set_error(W4A16_ERR_CONFIG, "%s: K=%d leaves a partial scale group of %d",
                          what, K, group);
     if (group % 8 != 0)
-        return set_error(W4A16_ERR_CONFIG, "%s: a group must be a multiple of 8; got %d", what,
+        return set_error(W4A16_ERR_CONFIG, "%s: group %d does not split into 8-code dwords", what,
                          group);
     if (group != W4A16_GROUP)
         return set_error(W4A16_ERR_CONFIG, "%s: the tile order holds 128-wide groups, not %d",
                          what, group);
     if (N % W4A16_TILE_ROWS != 0)
-        return set_error(W4A16_ERR_CONFIG, "%s: N=%d is not a whole number of 8-row tiles",
-                         what, N);
+        return set_error(W4A16_ERR_CONFIG, "%s: N=%d rows do not fill 8-row tiles", what, N);
     if (M == 1 && K > kMaxRowK)
         return set_error(W4A16_ERR_CONFIG, "%s: K=%d at M=1 needs more than 96 KiB of activation "
                          "staging (max K %d)", what, K, kMaxRowK);

@@ -49,9 +49,9 @@ float orc_bf16_to_f32(uint16_t bits) {
 
 /* reference csrc/linear_weight.cpp:57-86 */
 int orc_layout_check(long long n, long long k, long long group) {
-    if (n <= 0 || k <= 0) return fail(ORC_ERR_RANGE, "extents must be positive (n=%lld k=%lld)", n, k);
+    if (n <= 0 || k <= 0) return fail(ORC_ERR_RANGE, "empty or negative shape %lld x %lld", n, k);
     if (group != ORC_GROUP) return fail(ORC_ERR_RANGE, "group must be %d, got %lld", ORC_GROUP, group);
-    if (k % group) return fail(ORC_ERR_RANGE, "K=%lld is not a whole number of groups", k);
+    if (k % group) return fail(ORC_ERR_RANGE, "K=%lld is not a multiple of the group", k);
     if (n % ORC_TILE_ROWS) return fail(ORC_ERR_RANGE, "N=%lld is not a multiple of %d", n, ORC_TILE_ROWS);
     return ORC_OK;
 }
@@ -133,7 +133,7 @@ int orc_dequantize_int4(long long n, long long k, const uint8_t *packed, const u
                 const long long kk = g * ORC_GROUP + i;
                 const int nib = nibble_at(packed, r * k + kk);
                 if (nib == 0x8)
-                    return fail(ORC_ERR_FORMAT, "row %lld column %lld carries reserved code -8", r, kk);
+                    return fail(ORC_ERR_FORMAT, "code -8 at row %lld column %lld", r, kk);
                 out[r * k + kk] = (float)sext4(nib) * s;
             }
         }

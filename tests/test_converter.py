@@ -165,7 +165,7 @@ def test_flipped_byte_refused(converted, tmp_path):
         handle.seek(33)
         handle.write(bytes([b[0] ^ 0x10]))
     problems = convert.verify(path)
-    assert any("digest" in p for p in problems), problems
+    assert any("content hash" in p for p in problems), problems
     assert w4a16.artifact_verify(bad, victim["file"], "u8", victim["bytes"], victim["sha256"], "u8") == 6
     binary = oracle.ref_binary("quant_manifest_test")
     if binary:
@@ -196,7 +196,7 @@ def test_foreign_format_refused(converted, tmp_path):
     assert renamed != text
     with open(path, "w") as handle:
         handle.write(renamed)
-    assert any("format's name" in p for p in convert.verify(path))
+    assert any("format block: 'name'" in p for p in convert.verify(path))
     lib = oracle.ref_binary("libref_format.so")
     for needle, repl in (('"abi_version": 1', '"abi_version": 2'), ('"zero_point": 0', '"zero_point": 8')):
         foreign = text.replace(needle, repl, 1)
@@ -211,7 +211,7 @@ def test_foreign_format_refused(converted, tmp_path):
             assert ref.quant_manifest_parse(foreign.encode(), buf, err, 512) == 3
         with open(path, "w") as handle:
             handle.write(foreign)
-        assert any("format's" in p for p in convert.verify(path))
+        assert any("format block" in p for p in convert.verify(path))
         eng = w4a16.Engine(len(LAYER_FFNS), H, I, dense=[f == "dense" for f in LAYER_FFNS])
         assert eng.load_quantized_ffn(bad) == w4a16.W4A16_ERR_WEIGHTS
         assert "format" in eng.last_error(), eng.last_error()
@@ -243,7 +243,7 @@ def test_changed_source_refused(converted, tmp_path):
     with open(os.path.join(src, "model-00002.safetensors"), "r+b") as handle:
         handle.seek(-3, os.SEEK_END)
         handle.write(b"\x01\x02\x03")
-    assert any("source shard" in p for p in convert.verify(path))
+    assert any("source checkpoint" in p for p in convert.verify(path))
 
 
 def test_bad_checkpoints_refused(tmp_path):
@@ -251,7 +251,7 @@ def test_bad_checkpoints_refused(tmp_path):
     with pytest.raises(convert.ConvertError, match="BF16"):
         convert.convert_checkpoint(model, desc, str(tmp_path / "o1"))
     model, desc, _ = make_checkpoint(str(tmp_path / "dup"), duplicate=True)
-    with pytest.raises(convert.ConvertError, match="two shards"):
+    with pytest.raises(convert.ConvertError, match="stored by two shards"):
         convert.convert_checkpoint(model, desc, str(tmp_path / "o2"))
     model, desc, _ = make_checkpoint(str(tmp_path / "missing"))
     os.remove(os.path.join(model, "model-00001.safetensors"))
@@ -266,3 +266,31 @@ def test_sha256_file_in_blocks(tmp_path):
     p = tmp_path / "blob"
     p.write_bytes(data)
     assert convert.sha256_file(str(p), block=1 << 16) == hashlib.sha256(data).hexdigest()
+
+
+def test_audit_finds_table_mutants(converted, tmp_path):
+    """Mutants that pass the file pass (digests rewritten to match) and are caught by the table
+    pass: a pair whose payload is up rows then gate rows, a precision cell listed twice, a cell
+    dropped from the descriptor's grid, and an entry listed twice."""
+    bad, path = copy_out(converted, tmp_path)
+    with open(path) as handle:
+        doc = json.load(handle)
+    pair = doc["pairs"][0]
+    members = {e["role"]: e for e in doc["entries"] if e["layer"] == pair["layer"]}
+    swapped = b"".join(open(os.path.join(bad, members[r]["packed"]["file"]), "rb").read()
+                       for r in ("mlpUp", "mlpGate"))
+    with open(os.path.join(bad, pair["packed"]["file"]), "wb") as handle:
+        handle.write(swapped)
+    pair["packed"]["sha256"] = convert.sha256_file(os.path.join(bad, pair["packed"]["file"]))
+    doc["precision_map"].append(dict(doc["precision_map"][0]))
+    dropped = doc["precision_map"].pop(3)
+    doc["entries"].append(dict(doc["entries"][1]))
+    with open(path, "w") as handle:
+        json.dump(doc, handle, indent=2, sort_keys=True)
+    found = convert.verify(path)
+    assert any("not the gate rows followed by the up rows" in f for f in found), found
+    assert any("occurs 2 times" in f for f in found), found
+    assert any(f"no cell for the descriptor's layer {dropped['layer']} {dropped['role']}" in f
+               for f in found), found
+    assert any("more than one entry" in f for f in found), found
+    assert not any("content hash" in f for f in found), found
