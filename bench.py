@@ -11,8 +11,9 @@ gate/up/SiLU kernel + down kernel) on the next set, inputs already resident in H
 ``--config 2`` runs the 27B FFN (hidden 5120, intermediate 17408) over 64 distinct layers
 (8.8 GB); ``--config 4`` its tp=2 rank-0 slice; ``--config 0`` the single K=2560, N=9728
 linear; ``--config 3`` config 1 at M = --m; ``--config 5`` the single linear at the shape the
-reference publishes its one per-call INT4 figure for (N=4096, K=5120, M=1: 52.1 us, 207.6 GB/s
-on an A40, reference docs/plan-numeric-contract.md:1753), quoted beside this run's.
+reference publishes its per-call INT4 figures for (N=4096, K=5120: 52.1 us at M=1 on an A40,
+reference docs/plan-numeric-contract.md:1753, and its --time sweep at M = 2 / 16 / 64 / 128,
+:1775-1778), at M = --m or over --m-sweep, quoted beside this run's.
 
 Timing: the calls of one pass over the rotating sets are captured in a HIP graph (and the first
 steps % sets calls in a second graph); exactly --steps calls are replayed in the timed region,
@@ -20,10 +21,18 @@ with a HIP event on the replay stream before it and after every pass, so ``value
 time per call over all --steps calls (gaps between kernels included, not Python's launch rate)
 and ``config.pass_us_per_call`` gives the median, min and max over the passes.
 
-Prints ONE JSON line. ``roofline`` is the dominant kernel's (the fused gate/up/SiLU GEMV):
-algorithmic bytes per launch (packed nibbles + BF16 scales of its weight) over its average
-launch duration, from a graph holding only that kernel's launches, timed the same way.
-``cpu_baseline`` times the CPU dequant+matmul path (numpy, BLAS) over a bounded sample.
+Prints ONE JSON line.
+* ``roofline`` is the dominant kernel's (the fused gate/up/SiLU GEMV, or the linear):
+  algorithmic bytes per launch (packed nibbles + BF16 scales of its weight) over its average
+  duration, measured live: --steps eager calls, the kernel's dispatch in each timed by the
+  start/end events of w4a16_time_next_launch (hipExtLaunchKernel), which are the dispatch's own
+  times, the ones a kernel trace reports. ``rocprof_avg_us`` / ``frac_from_rocprof`` quote the
+  committed rocprofv3 kernel-trace average of the same workload (profiles/) beside it.
+* ``floor_us`` / ``floor`` (FFN configs): a pure streaming read of the call's bytes in one
+  launch, as two dependent launches, and an empty launch pair, on the same rotation
+  (libw4a16_floor.so).
+* ``secondary`` (config 1): config 3's verify rows M = 2, 4, 8, 16 on the same weight sets.
+* ``cpu_baseline`` times the CPU dequant+matmul path (numpy, BLAS) over a bounded sample.
 """
 
 import argparse
@@ -40,6 +49,7 @@ for _p in (ROOT, PKG):
 
 HBM_PEAK_GBS = 8000.0
 CACHE_ROTATE_BYTES = 512 << 20   # rotate at least this many weight bytes (MALL is 256 MB)
+KERNEL_TIMING_CHUNK = 32         # eager calls enqueued behind one spin kernel (kernel_us)
 
 
 def parse():
@@ -48,7 +58,13 @@ def parse():
     ap.add_argument("--steps", type=int, default=512)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3, 4, 5))
-    ap.add_argument("--m", type=int, default=4, help="rows for --config 3")
+    ap.add_argument("--m", type=int, default=None,
+                    help="activation rows: --config 3 (default 4) and --config 5 (default 1)")
+    ap.add_argument("--m-sweep", default=None,
+                    help="--config 5 only: comma-separated row counts (e.g. 1,2,4,8,16,32,64,128), "
+                         "each timed like the main line and reported in `sweep`")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="config 1: skip the C3 verify-row timings reported in `secondary`")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--pmc-pass", action="store_true",
@@ -68,7 +84,8 @@ def shapes(cfg, m):
     if cfg == 3:
         return 2560, 9728, m, f"config3: Qwen3-4B dense FFN verify rows M={m}"
     if cfg == 5:
-        return 5120, 4096, 1, "config5: the reference's published shape, W4A16 linear M=1 K=5120 N=4096"
+        return 5120, 4096, m, (f"config5: the reference's published shape, W4A16 linear M={m} "
+                               f"K=5120 N=4096")
     return 5120, 8704, 1, "config4: tp=2 rank-0 slice of config2 (I/2=8704), FP32 partial"
 
 
@@ -163,6 +180,51 @@ def cpu_baseline(sets, hidden, inter, m, linear_only, seconds):
                                       f"dequantized once, median"}}
 
 
+class HipEvents:
+    """hipEvent_t handles from the HIP runtime the process already loaded (torch's and the
+    library's are one: same soname), for w4a16_time_next_launch."""
+
+    def __init__(self):
+        import ctypes
+
+        self.ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+
+    def create(self, n):
+        out = []
+        for _ in range(n):
+            h = self.ct.c_void_p()
+            if self.hip.hipEventCreate(self.ct.byref(h)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            out.append(h.value)
+        return out
+
+    def elapsed_us(self, a, b):
+        self.hip.hipEventSynchronize(b)
+        ms = self.ct.c_float()
+        if self.hip.hipEventElapsedTime(self.ct.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value * 1e3
+
+    def destroy(self, handles):
+        for h in handles:
+            self.hip.hipEventDestroy(h)
+
+
+def profile_json(kind, tag):
+    """The committed rocprofv3 figures of one workload (profiles/<kind>_<tag>.json), or {}."""
+    path = os.path.join(ROOT, "profiles", f"{kind}_{tag}.json")
+    if not os.path.exists(path):
+        return {}, None
+    with open(path) as handle:
+        return json.load(handle), os.path.relpath(path, ROOT)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -170,7 +232,12 @@ def main():
               "(the tensor-parallel slice is benchmarked on one GPU as --config 4)",
               file=sys.stderr)
         sys.exit(2)
-    import numpy as np
+    if args.m is None:
+        args.m = 4 if args.config == 3 else 1
+    if args.m != 1 and args.config not in (3, 5):
+        sys.exit("bench.py: --m applies to --config 3 and --config 5")
+    if args.m_sweep and args.config != 5:
+        sys.exit("bench.py: --m-sweep applies to --config 5")
     import torch
 
     import w4a16
@@ -189,30 +256,36 @@ def main():
     sets = make_sets(torch, w4a16, hidden, inter, count, linear_only)
     gen = torch.Generator(device=dev)
     gen.manual_seed(7)
-    x = torch.randn(m, hidden, generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
-    act = torch.empty(m, inter, dtype=torch.int16, device=dev)
     partial = args.config == 4
-    out = torch.empty(m, inter if linear_only else hidden,
-                      dtype=torch.float32 if partial else torch.int16, device=dev)
-    down_out = torch.empty(m, hidden, dtype=torch.int16, device=dev)
+    events = HipEvents()
 
-    def ffn_call(i):
-        gu, dn, _ = sets[i % count]
-        if linear_only:
-            w4a16.gemm_int4_bf16(x, gu, out)
-        else:
-            w4a16.mlp_int4(x, gu, dn, out=out, act_ws=act, partial_f32=partial)
+    def buffers(rows):
+        x = torch.randn(rows, hidden, generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
+        act = torch.empty(rows, inter, dtype=torch.int16, device=dev)
+        out = torch.empty(rows, inter if linear_only else hidden,
+                          dtype=torch.float32 if partial else torch.int16, device=dev)
+        return x, act, out
 
-    def first_kernel(i):
-        gu = sets[i % count][0]
-        if linear_only:
-            w4a16.gemm_int4_bf16(x, gu, out)
-        else:
-            w4a16.gate_up_silu(x, gu, act)
+    x, act, out = buffers(m)
 
-    def second_kernel(i):
-        if not linear_only:
-            w4a16.gemm_int4_bf16(act, sets[i % count][1], down_out)
+    def make_calls(x, act, out):
+        def ffn_call(i):
+            gu, dn, _ = sets[i % count]
+            if linear_only:
+                w4a16.gemm_int4_bf16(x, gu, out)
+            else:
+                w4a16.mlp_int4(x, gu, dn, out=out, act_ws=act, partial_f32=partial)
+
+        def first_kernel(i):
+            gu = sets[i % count][0]
+            if linear_only:
+                w4a16.gemm_int4_bf16(x, gu, out)
+            else:
+                w4a16.gate_up_silu(x, gu, act)
+
+        return ffn_call, first_kernel
+
+    ffn_call, first_kernel = make_calls(x, act, out)
 
     # Launches are captured into HIP graphs (one graph = one pass over all rotating weight sets,
     # plus one holding the first steps % count calls) so the timed region measures the device,
@@ -241,18 +314,53 @@ def main():
         torch.cuda.synchronize()
         stream = torch.cuda.current_stream()
         passes = [(full, count)] * (steps // count) + ([(tail, rest)] if tail else [])
-        events = [torch.cuda.Event(enable_timing=True) for _ in range(len(passes) + 1)]
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(len(passes) + 1)]
         t0 = time.perf_counter()
-        events[0].record(stream)
+        evs[0].record(stream)
         for i, (graph, _) in enumerate(passes):
             graph.replay()
-            events[i + 1].record(stream)
+            evs[i + 1].record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        per_pass = [events[i].elapsed_time(events[i + 1]) * 1e3 / n
-                    for i, (_, n) in enumerate(passes)]
-        total_us = events[0].elapsed_time(events[-1]) * 1e3
+        per_pass = [evs[i].elapsed_time(evs[i + 1]) * 1e3 / n for i, (_, n) in enumerate(passes)]
+        total_us = evs[0].elapsed_time(evs[-1]) * 1e3
         return total_us / steps, wall * 1e6 / steps, per_pass
+
+    spin_cycles_per_us = []
+
+    def busy_stream(us):
+        """Hold the current stream for about `us` microseconds (torch's spin kernel)."""
+        if not spin_cycles_per_us:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(1000)
+            a.record()
+            torch.cuda._sleep(1 << 20)
+            b.record()
+            torch.cuda.synchronize()
+            spin_cycles_per_us.append((1 << 20) / max(a.elapsed_time(b) * 1e3, 1.0))
+        torch.cuda._sleep(int(spin_cycles_per_us[0] * us))
+
+    def kernel_us(fn, steps, warmup, skip=0):
+        """Average duration of the kernel fn launches after `skip` others, over `steps` eager
+        calls (after `warmup`), each timed by the events of w4a16_time_next_launch on the stream
+        it runs on: the dispatch's own start and end, as a kernel trace reports them."""
+        for i in range(max(warmup, 1)):
+            fn(i)
+        torch.cuda.synchronize()
+        handles = events.create(2 * steps)
+        for i in range(steps):
+            if i % KERNEL_TIMING_CHUNK == 0:
+                # A host-side launch takes longer than the call runs, so the stream would drain
+                # between eager calls and each kernel would start on an idle GPU. A spin kernel
+                # ahead of every chunk holds the stream while the chunk's calls are enqueued;
+                # they then run back to back, as in the graph-replayed call.
+                busy_stream(KERNEL_TIMING_CHUNK * 60.0)
+            w4a16.lib.w4a16_time_next_launch(skip, handles[2 * i], handles[2 * i + 1])
+            fn(i)
+        torch.cuda.synchronize()
+        total = sum(events.elapsed_us(handles[2 * i], handles[2 * i + 1]) for i in range(steps))
+        events.destroy(handles)
+        return total / steps
 
     if args.pmc_pass:
         for i in range(args.steps):
@@ -269,10 +377,11 @@ def main():
         sys.exit("bench.py: --steps must be at least 1")
     us_per_call, wall_us, per_pass = timed(ffn_call, args.steps, args.warmup)
     ms_total = us_per_call * args.steps / 1e3
-    k1_avg, _, _ = timed(first_kernel, args.steps, args.warmup)
-    k2_avg = 0.0
+    k1_graph, _, _ = timed(first_kernel, args.steps, args.warmup)
+    k1_live = kernel_us(ffn_call, args.steps, args.warmup)              # the call's first kernel
+    k2_live = 0.0
     if not linear_only:
-        k2_avg, _, _ = timed(second_kernel, args.steps, args.warmup)
+        k2_live = kernel_us(ffn_call, args.steps, args.warmup, skip=1)   # the call's down kernel
     norm_us = f2_us = None
     if not linear_only:
         # forward_mlp: the same call with the post-attention RMSNorm folded in (plain style)
@@ -305,24 +414,20 @@ def main():
     else:
         dom_bytes = 2 * inter * hidden // 2 + 2 * inter * hidden // 128 * 2
         dom_role = "fused gate/up + SiLU x up"
-    achieved = dom_bytes / (k1_avg * 1e-6) / 1e9
-    tag = f"config{args.config}" + (f"_m{m}" if args.config == 3 else "")
+    down_bytes = inter * hidden // 2 + inter * hidden // 128 * 2
+    achieved = dom_bytes / (k1_live * 1e-6) / 1e9
+    tag = f"config{args.config}" + (f"_m{m}" if args.config == 3 or (args.config == 5 and m != 1)
+                                    else "")
     # The committed rocprofv3 summaries of the same configuration (profiles/): the kernel the
-    # dominant launch runs and its kernel-trace average (a cross-check of the live event timing
-    # above), and its HBM bytes per launch from FETCH_SIZE / WRITE_SIZE scaled by a plain copy.
-    dom_kernel, rocprof_avg, rocprof_src, traffic, traffic_src = None, None, None, None, None
-    kpath = os.path.join(ROOT, "profiles", f"kernel_avg_{tag}.json")
-    if os.path.exists(kpath):
-        with open(kpath) as handle:
-            dom = json.load(handle).get("dominant", {})
-        dom_kernel, rocprof_avg = dom.get("kernel"), dom.get("avg_us")
-        rocprof_src = os.path.relpath(kpath, ROOT)
-    tpath = os.path.join(ROOT, "profiles", f"traffic_{tag}.json")
-    if os.path.exists(tpath):
-        with open(tpath) as handle:
-            dom = json.load(handle).get("dominant", {})
-        traffic = dom.get("traffic_bytes")
-        traffic_src = os.path.relpath(tpath, ROOT) if traffic else None
+    # dominant launch runs and its kernel-trace average (which the live figure above must agree
+    # with), and its HBM bytes per launch from FETCH_SIZE / WRITE_SIZE scaled by a plain copy.
+    kdoc, rocprof_src = profile_json("kernel_avg", tag)
+    dom_kernel = kdoc.get("dominant", {}).get("kernel")
+    rocprof_avg = kdoc.get("dominant", {}).get("avg_us")
+    tdoc, traffic_src = profile_json("traffic", tag)
+    traffic = tdoc.get("dominant", {}).get("traffic_bytes")
+    if not traffic:
+        traffic_src = None
     dom_name = f"{dom_kernel or 'gemv'} ({dom_role})"
     ffn_gbs = per_set / (us_per_call * 1e-6) / 1e9
     srt = sorted(per_pass)
@@ -330,7 +435,7 @@ def main():
                   "min": round(srt[0], 3), "max": round(srt[-1], 3)}
 
     result = {
-        "metric": "\u00b5s per INT4 FFN decode call (M=1) + achieved HBM GB/s vs peak, 1 MI355X",
+        "metric": "µs per INT4 FFN decode call (M=1) + achieved HBM GB/s vs peak, 1 MI355X",
         "value": round(us_per_call, 3),
         "unit": "us per FFN call" if not linear_only else "us per linear call",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -345,32 +450,153 @@ def main():
                    "ffn_frac_of_peak": round(ffn_gbs / HBM_PEAK_GBS, 4),
                    "wall_us_per_call": round(wall_us, 3),
                    "pass_us_per_call": pass_stats,
-                   "kernel_avg_us": {"dominant": round(k1_avg, 3), "second": round(k2_avg, 3)},
-                   # the down projection is timed through gemm_int4_bf16 on row-major rows;
-                   # from M = 4 the FFN call runs it on its chunk-major intermediate instead
-                   **({"second_as_timed": "gemm_int4_bf16 (row-major rows), not the FFN's "
-                       "chunk-major down kernel"} if 4 <= m <= 16 and not linear_only else {}),
+                   "kernel_avg_us": {"dominant": round(k1_live, 3), "second": round(k2_live, 3),
+                                     "source": "live: per-launch dispatch events "
+                                               "(w4a16_time_next_launch), eager launches"},
                    "with_rmsnorm_us_per_call": None if norm_us is None else round(norm_us, 3),
                    "with_residual_rmsnorm_us_per_call": None if f2_us is None else round(f2_us, 3)},
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": traffic_src, "bytes_per_launch": dom_bytes,
-                     "avg_launch_us": round(k1_avg, 3), "rocprof_avg_us": rocprof_avg,
-                     "rocprof_source": rocprof_src,
+                     "avg_launch_us": round(k1_live, 3),
+                     "avg_launch_source": "live: dispatch start/end events of each launch, eager calls "
+                                          "enqueued back to back behind a spin kernel",
+                     "graph_us_per_launch": round(k1_graph, 3),
+                     "rocprof_avg_us": rocprof_avg, "rocprof_source": rocprof_src,
                      "frac_from_rocprof": None if not rocprof_avg else
                      round(dom_bytes / (rocprof_avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
     }
+    if not linear_only:
+        floor = floor_us(torch, dev, count, dom_bytes, down_bytes, events, timed_fn=timed,
+                         steps=args.steps, warmup=args.warmup)
+        result["floor_us"] = floor["one_launch_read_us"]
+        result["floor"] = floor
     if args.config == 5:
-        # the reference's own per-call figure at this shape, on its hardware (A40, ~696 GB/s)
+        # the reference's own per-call figures at this shape, on its hardware (A40, ~696 GB/s)
+        pub = {1: 52.1, 2: 924.1, 16: 996.7, 64: 2247.7, 128: 3316.1}
         result["config"]["reference_published"] = {
-            "us_per_call": 52.1, "GBps": 207.6, "hardware": "NVIDIA A40",
-            "frac_of_its_peak": round(207.6 / 696.0, 3),
-            "source": "reference docs/plan-numeric-contract.md:1753, docs/worklog.md:514"}
+            "us_per_call": pub.get(m), "GBps": 207.6 if m == 1 else None,
+            "hardware": "NVIDIA A40", "frac_of_its_peak": round(207.6 / 696.0, 3) if m == 1 else None,
+            "source": "reference docs/plan-numeric-contract.md:1753 (M=1), :1775-1778 (M=2, 16, "
+                      "64, 128), docs/worklog.md:514"}
+        if args.m_sweep:
+            result["sweep"] = m_sweep(torch, w4a16, sets, count, hidden, inter, gen, dev,
+                                      [int(v) for v in args.m_sweep.split(",")], capture,
+                                      kernel_us, args, pub)
+    if args.config == 1 and not args.no_secondary:
+        result["secondary"] = secondary_rows(torch, w4a16, sets, count, hidden, inter, gen, dev,
+                                             timed, kernel_us, args, dom_bytes)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(sets, hidden, inter, m, linear_only,
                                               args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def floor_us(torch, dev, count, gu_bytes, dn_bytes, events, timed_fn, steps, warmup):
+    """What any implementation of the call can reach here, on buffers of the call's byte counts
+    rotated like the weight sets (libw4a16_floor.so): one launch reading both operands, the two
+    operands as two dependent launches, and a pair of empty dependent launches (graph-replayed,
+    as the call is). Each as us per call."""
+    import ctypes
+
+    floor = ctypes.CDLL(os.path.join(PKG, "libw4a16_floor.so"))
+    floor.w4a16_floor_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                       ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    floor.w4a16_floor_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    gu_b, dn_b = -(-gu_bytes // 16) * 16, -(-dn_bytes // 16) * 16
+    bufs = [(torch.full((gu_b,), 17, dtype=torch.uint8, device=dev),
+             torch.full((dn_b,), 23, dtype=torch.uint8, device=dev)) for _ in range(count)]
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+
+    def stream():
+        return torch.cuda.current_stream().cuda_stream
+
+    def one(i):
+        a, b = bufs[i % count]
+        floor.w4a16_floor_read(a.data_ptr(), gu_b, b.data_ptr(), dn_b, sink.data_ptr(), stream())
+
+    def two(i):
+        a, b = bufs[i % count]
+        floor.w4a16_floor_read(a.data_ptr(), gu_b, None, 0, sink.data_ptr(), stream())
+        floor.w4a16_floor_read(b.data_ptr(), dn_b, None, 0, sink.data_ptr(), stream())
+
+    def empty(i):
+        floor.w4a16_floor_empty(2, 256, 256, stream())
+
+    res = {}
+    for key, fn in (("one_launch_read_us", one), ("two_launch_read_us", two),
+                    ("empty_launch_pair_us", empty)):
+        res[key] = round(timed_fn(fn, steps, warmup)[0], 3)
+    res["bytes"] = [gu_bytes, dn_bytes]
+    res["note"] = ("pure streaming reads of the call's weight bytes (non-temporal 16-byte loads, "
+                   "all of a lane's loads issued first), rotated over the same number of sets, "
+                   "graph-replayed like the call; libw4a16_floor.so")
+    del bufs
+    return res
+
+
+def secondary_rows(torch, w4a16, sets, count, hidden, inter, gen, dev, timed, kernel_us, args,
+                   dom_bytes):
+    """Config 3 on config 1's weight sets: the FFN call at M = 2, 4, 8, 16 verify rows, us per
+    call (graph-replayed, --steps calls), the live average of its gate/up kernel and that
+    kernel's fraction of peak, beside the committed rocprofv3 figure of the same workload."""
+    rows = {}
+    for mm in (2, 4, 8, 16):
+        x = torch.randn(mm, hidden, generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
+        act = torch.empty(mm, inter, dtype=torch.int16, device=dev)
+        out = torch.empty(mm, hidden, dtype=torch.int16, device=dev)
+
+        def call(i, x=x, act=act, out=out):
+            gu, dn, _ = sets[i % count]
+            w4a16.mlp_int4(x, gu, dn, out=out, act_ws=act)
+
+        us, _, _ = timed(call, args.steps, args.warmup)
+        k1 = kernel_us(call, args.steps, args.warmup)      # the call's gate/up kernel
+        kdoc, src = profile_json("kernel_avg", f"config3_m{mm}")
+        rp = kdoc.get("dominant", {}).get("avg_us")
+        rows[f"M={mm}"] = {
+            "us_per_call": round(us, 3),
+            "GBps_whole_call": round(3 * dom_bytes / 2 / (us * 1e-6) / 1e9, 1),
+            "gate_up_us_live": round(k1, 3),
+            "gate_up_frac_live": round(dom_bytes / (k1 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "gate_up_kernel": kdoc.get("dominant", {}).get("kernel"),
+            "gate_up_rocprof_avg_us": rp, "rocprof_source": src,
+            "gate_up_frac_from_rocprof": None if not rp else
+            round(dom_bytes / (rp * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    return {"workload": "config3: config 1's weight sets with M verify rows", "rows": rows}
+
+
+def m_sweep(torch, w4a16, sets, count, hidden, inter, gen, dev, ms, capture, kernel_us, args, pub):
+    """The reference's --time sweep shape (N=4096, K=5120) at each M: us per linear call
+    (graph-replayed over the rotating sets, --steps calls) and live kernel average."""
+    rows = {}
+    per_set = inter * hidden // 2 + inter * hidden // 128 * 2
+    for mm in ms:
+        x = torch.randn(mm, hidden, generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
+        out = torch.empty(mm, inter, dtype=torch.int16, device=dev)
+
+        def call(i, x=x, out=out):
+            w4a16.gemm_int4_bf16(x, sets[i % count][0], out)
+
+        graph = capture(call)
+        for _ in range(2):
+            graph.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = max(1, args.steps // count)
+        a.record()
+        for _ in range(reps):
+            graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / (reps * count)
+        k = kernel_us(call, args.steps, args.warmup)
+        rows[f"M={mm}"] = {"us_per_call": round(us, 3), "kernel_us_live": round(k, 3),
+                           "GBps": round(per_set / (us * 1e-6) / 1e9, 1),
+                           "frac_of_peak": round(per_set / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                           "reference_A40_us": pub.get(mm)}
+    return rows
 
 
 if __name__ == "__main__":

@@ -37,6 +37,7 @@
  *   tile_pack_kernel, dequant_tiled_kernel, quantize_kernel: the load-time re-layout and the
  *                       checks of it
  */
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -510,14 +511,30 @@ __device__ __forceinline__ uint64_t slot_peek(const uint64_t *slot) {
     return __hip_atomic_load(const_cast<uint64_t *>(slot), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-/* The value of a slot whose first read was `w`, waiting for its flag if needed; clears it. */
-__device__ __forceinline__ float slot_take(uint64_t *slot, uint64_t w) {
-    for (int n = 0; (w >> 32) == 0 && n < kSlotWaitPolls; ++n) {
+/* Bounded waits that gave up since the host last read this word (per device; read and cleared
+ * by w4a16_split_wait_status). A wait that gives up means a combine summed a slot that was never
+ * written, so the call's output is wrong: the count turns that into an error the host can see. */
+__device__ unsigned g_slot_wait_timeouts;
+
+/* The value of a slot whose first read was `w`, waiting (at most `polls` polls) for its flag if
+ * needed; clears it. A wait that gives up counts itself in g_slot_wait_timeouts and returns 0. */
+__device__ __forceinline__ float slot_take(uint64_t *slot, uint64_t w, int polls = kSlotWaitPolls) {
+    for (int n = 0; (w >> 32) == 0 && n < polls; ++n) {
         __builtin_amdgcn_s_sleep(1);
         w = slot_peek(slot);
     }
+    if ((w >> 32) == 0) {
+        __hip_atomic_fetch_add(&g_slot_wait_timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        w = 0;
+    }
     __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return __uint_as_float((uint32_t)w);
+}
+
+/* One wave waiting on the slot at `slot` with the given poll bound (status path test). */
+__global__ __launch_bounds__(64) void slot_wait_probe_kernel(uint64_t *slot, int polls, float *out) {
+    const float v = slot_take(slot, slot_peek(slot), polls);
+    if (threadIdx.x == 0) out[0] = v;
 }
 
 /* Counts one block's arrival (lane 0) and returns the count before it on every lane. */
@@ -1610,6 +1627,29 @@ int hip_status(hipError_t e, const char *what) {
     return set_error(W4A16_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+/* Events that time one of the calling thread's next kernel launches (w4a16_time_next_launch): it
+ * goes through hipExtLaunchKernel, whose events take the dispatch's own start and end times
+ * (the times a kernel trace reports), and the pair is then forgotten. */
+thread_local hipEvent_t t_next_launch_events[2] = {nullptr, nullptr};
+thread_local int t_launches_to_skip = 0;
+
+template <typename... Params, typename... Args>
+void launch_k(void (*kernel)(Params...), dim3 grid, dim3 block, size_t smem, hipStream_t stream,
+              Args... args) {
+    hipEvent_t start = t_next_launch_events[0], stop = t_next_launch_events[1];
+    if ((start || stop) && t_launches_to_skip > 0) {
+        --t_launches_to_skip;
+        start = stop = nullptr;
+    }
+    if (start || stop) {
+        t_next_launch_events[0] = t_next_launch_events[1] = nullptr;
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)smem, stream, start, stop, 0u,
+                              static_cast<Params>(args)...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, smem, stream, static_cast<Params>(args)...);
+    }
+}
+
 int grid_for(long long work, int block) {
     long long g = (work + block - 1) / block;
     if (g > 65535LL * 16) g = 65535LL * 16;
@@ -1635,11 +1675,11 @@ int launch_gemv_cfg(const uint16_t *x, const uint8_t *w, const uint16_t *s, void
         return set_error(W4A16_ERR_CONFIG, "internal: a %d x %d gemv shape covers %d of %d group pairs",
                          SK, NL, SK * NL, (K / 128 + 1) / 2);
     if (norm)
-        hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK, true, NL>),
+        launch_k((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK, true, NL>),
                            dim3((tiles + TB - 1) / TB), dim3(TB * SK * 64), gemv_smem(K, TB * SK),
                            stream, x, w, s, out, N, K, norm->w, norm->bias, norm->eps, norm->sub);
     else
-        hipLaunchKernelGGL((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK, false, NL>),
+        launch_k((gemv_tiles_kernel<PAIR, OUT_F32, TB, SK, false, NL>),
                            dim3((tiles + TB - 1) / TB), dim3(TB * SK * 64), gemv_smem(K, TB * SK),
                            stream, x, w, s, out, N, K, nullptr, 0.0f, 0.0f, nullptr);
     return hip_status(hipGetLastError(), "gemv launch");
@@ -1661,7 +1701,7 @@ int launch_xwave_np(const uint16_t *x, const uint8_t *w, const uint16_t *s, void
                                &partial, &counters);
         if (st) return st;
     }
-    hipLaunchKernelGGL((gemv_xwave_kernel<PAIR, OUT_F32, SK, NP, BS>), dim3(N / 8 * BS), dim3(SK * 64),
+    launch_k((gemv_xwave_kernel<PAIR, OUT_F32, SK, NP, BS>), dim3(N / 8 * BS), dim3(SK * 64),
                        xwave_smem(SK, NP), stream, x, w, s, out, N, K, partial, counters, residual,
                        sub);
     return hip_status(hipGetLastError(), "gemv launch");
@@ -1673,7 +1713,7 @@ int launch_mfma1(const uint16_t *x, const uint8_t *w, const uint16_t *s, void *o
     if (SK * NP < (K / 128 + 1) / 2)
         return set_error(W4A16_ERR_CONFIG, "internal: a %d x %d matrix-core gemv shape covers %d of %d "
                          "group pairs", SK, NP, SK * NP, (K / 128 + 1) / 2);
-    hipLaunchKernelGGL((gemv_mfma1_kernel<PAIR, OUT_F32, SK, NP, M>), dim3(N / 8), dim3(SK * 64),
+    launch_k((gemv_mfma1_kernel<PAIR, OUT_F32, SK, NP, M>), dim3(N / 8), dim3(SK * 64),
                        mfma1_smem(SK, NP, M), stream, x, w, s, out, N, K, residual, sub);
     return hip_status(hipGetLastError(), "gemv launch");
 }
@@ -1784,10 +1824,10 @@ int launch_rows_mi(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s
     if (smem > kMaxLds) return 1;
     const dim3 grid((N / 8 + TB - 1) / TB), block(TB * SK * 64);
     if (M == 2)
-        hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 2>), grid, block, smem,
+        launch_k((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 2>), grid, block, smem,
                            stream, x, M, w, s, out, N, K, residual, cm);
     else
-        hipLaunchKernelGGL((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 4>), grid, block, smem,
+        launch_k((gemv_rows_kernel<PAIR, OUT_F32, TB, SK, NL, 4>), grid, block, smem,
                            stream, x, M, w, s, out, N, K, residual, cm);
     return hip_status(hipGetLastError(), "gemv rows launch");
 }
@@ -1814,7 +1854,7 @@ int launch_rows16_nl(const uint16_t *x, int M, const uint8_t *w, const uint16_t 
     const size_t smem = rows16_smem(M, K, TP * SK);
     if (smem > kMaxLds) return 1;
     const int pairs = (N / 8 + 1) / 2;
-    hipLaunchKernelGGL((gemv_rows16_kernel<PAIR, OUT_F32, NL>), dim3((pairs + TP - 1) / TP),
+    launch_k((gemv_rows16_kernel<PAIR, OUT_F32, NL>), dim3((pairs + TP - 1) / TP),
                        dim3(TP * SK * 64), smem, stream, x, M, w, s, out, N, K, TP, SK, cm);
     return hip_status(hipGetLastError(), "gemv rows16 launch");
 }
@@ -1826,7 +1866,7 @@ int launch_rows16x_nl(const uint16_t *x, int M, const uint8_t *w, const uint16_t
                       int N, int K, hipStream_t stream, uint16_t *residual) {
     constexpr int D = NL <= 5 ? NL : NL <= 9 ? 4 : 3;
     const int pairs = (N / 8 + 1) / 2;
-    hipLaunchKernelGGL((gemv_rows16x_kernel<OUT_F32, NL, D, CM>), dim3(pairs), dim3(1024), 0, stream,
+    launch_k((gemv_rows16x_kernel<OUT_F32, NL, D, CM>), dim3(pairs), dim3(1024), 0, stream,
                        x, M, w, s, out, N, K, residual);
     return hip_status(hipGetLastError(), "gemv rows16x launch");
 }
@@ -2054,7 +2094,7 @@ int fixed_scratch(hipStream_t stream, unsigned char **base) {
         st = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
         if (st) return st;
         if (!p) return set_error(W4A16_ERR_HIP, "hipGetSymbolAddress(scratch) returned no address");
-        hipLaunchKernelGGL(zero_words_kernel, dim3(2048), dim3(256), 0, stream,
+        launch_k(zero_words_kernel, dim3(2048), dim3(256), 0, stream,
                            static_cast<unsigned *>(p), sizeof(scratch) / 4);
         st = hip_status(hipGetLastError(), "scratch clear");
         if (st) return st;
@@ -2082,15 +2122,15 @@ int launch_mfma_x(const MfmaPlan &p, const uint16_t *x, int M, const uint8_t *w,
                   const uint16_t *s, void *out, int N, int K, uint64_t *partial, unsigned *counters,
                   hipStream_t stream, uint16_t *residual, int cm) {
     if (M == 1)
-        hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE, 1>), dim3(p.grid), dim3(kMfmaWaves * 64),
+        launch_k((mfma_gemm_kernel<OUT, XPRE, 1>), dim3(p.grid), dim3(kMfmaWaves * 64),
                            p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters,
                            residual, cm);
     else if (M == 2)
-        hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE, 2>), dim3(p.grid), dim3(kMfmaWaves * 64),
+        launch_k((mfma_gemm_kernel<OUT, XPRE, 2>), dim3(p.grid), dim3(kMfmaWaves * 64),
                            p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters,
                            residual, cm);
     else
-        hipLaunchKernelGGL((mfma_gemm_kernel<OUT, XPRE, 4>), dim3(p.grid), dim3(kMfmaWaves * 64),
+        launch_k((mfma_gemm_kernel<OUT, XPRE, 4>), dim3(p.grid), dim3(kMfmaWaves * 64),
                            p.smem, stream, x, M, w, s, out, N, K, p.S, p.GS, partial, counters,
                            residual, cm);
     return hip_status(hipGetLastError(), "mfma gemm launch");
@@ -2319,10 +2359,10 @@ static int launch_rmsnorm(uint16_t *out, const uint16_t *x, const uint16_t *w, i
     if (cols % 8 || ch > 8)
         return set_error(W4A16_ERR_CONFIG, "rmsnorm: cols=%d must be a multiple of 8 and <= 16384",
                          cols);
-    if (ch <= 1) hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(rows), dim3(256), 0, s, out, const_cast<uint16_t *>(x), w, cols, bias, eps, sub);
-    else if (ch <= 2) hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3(rows), dim3(256), 0, s, out, const_cast<uint16_t *>(x), w, cols, bias, eps, sub);
-    else if (ch <= 4) hipLaunchKernelGGL(rmsnorm_kernel<4>, dim3(rows), dim3(256), 0, s, out, const_cast<uint16_t *>(x), w, cols, bias, eps, sub);
-    else hipLaunchKernelGGL(rmsnorm_kernel<8>, dim3(rows), dim3(256), 0, s, out, const_cast<uint16_t *>(x), w, cols, bias, eps, sub);
+    if (ch <= 1) launch_k(rmsnorm_kernel<1>, dim3(rows), dim3(256), 0, s, out, const_cast<uint16_t *>(x), w, cols, bias, eps, sub);
+    else if (ch <= 2) launch_k(rmsnorm_kernel<2>, dim3(rows), dim3(256), 0, s, out, const_cast<uint16_t *>(x), w, cols, bias, eps, sub);
+    else if (ch <= 4) launch_k(rmsnorm_kernel<4>, dim3(rows), dim3(256), 0, s, out, const_cast<uint16_t *>(x), w, cols, bias, eps, sub);
+    else launch_k(rmsnorm_kernel<8>, dim3(rows), dim3(256), 0, s, out, const_cast<uint16_t *>(x), w, cols, bias, eps, sub);
     return hip_status(hipGetLastError(), "rmsnorm launch");
 }
 
@@ -2475,7 +2515,7 @@ extern "C" int mlp_int4_residual_norm_bf16(uint16_t *residual, const uint16_t *s
     st = run_rows<kOutBf16>(act, M, dnp, dns, out, hidden, inter, s);
     if (st) return st;
     const long long chunks = (long long)M * hidden / 8;
-    hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, s,
+    launch_k(residual_add_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, s,
                        residual, out, chunks);
     return hip_status(hipGetLastError(), "residual add launch");
 }
@@ -2498,7 +2538,7 @@ extern "C" int silu_mul_packed_bf16(uint16_t *out, const uint16_t *packed, int t
     if (misaligned(out) || misaligned(packed))
         return set_error(W4A16_ERR_CONFIG, "silu_mul_packed: buffers must be 16-byte aligned");
     const int block = 256;
-    hipLaunchKernelGGL(silu_mul_packed_kernel, dim3((inter + block - 1) / block, tokens),
+    launch_k(silu_mul_packed_kernel, dim3((inter + block - 1) / block, tokens),
                        dim3(block), 0, static_cast<hipStream_t>(stream), out, packed, tokens,
                        inter);
     return hip_status(hipGetLastError(), "silu_mul_packed launch");
@@ -2515,7 +2555,7 @@ extern "C" int w4a16_tile_pack_device(long long n, long long k, int pair, const 
     if (st) return st;
     if (pair != 0 && pair != 1) return set_error(W4A16_ERR_CONFIG, "tile_pack_device: bad pair");
     const long long total = (n / 8) * (k / 128) * 128;
-    hipLaunchKernelGGL(tile_pack_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
+    launch_k(tile_pack_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), packed, scales,
                        reinterpret_cast<uint32_t *>(packed_tiled), scales_tiled, n, k, pair);
     return hip_status(hipGetLastError(), "tile_pack launch");
@@ -2533,7 +2573,7 @@ extern "C" int w4a16_dequant_tiled_device(long long n, long long k, int pair,
     if (st) return st;
     if (pair != 0 && pair != 1) return set_error(W4A16_ERR_CONFIG, "dequant_tiled: bad pair");
     const long long total = (n / 8) * (k / 128) * 128;
-    hipLaunchKernelGGL(dequant_tiled_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
+    launch_k(dequant_tiled_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream),
                        reinterpret_cast<const uint32_t *>(packed_tiled), scales_tiled, out, n, k,
                        pair);
@@ -2550,8 +2590,51 @@ extern "C" int w4a16_quantize_device(long long n, long long k, const float *weig
     int st = w4a16_layout_init(n, k, W4A16_GROUP, nullptr, nullptr);
     if (st) return st;
     const long long total = n * (k / 128);
-    hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
+    launch_k(quantize_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), weights, packed, scales, status_dev, n,
                        k);
     return hip_status(hipGetLastError(), "quantize launch");
+}
+
+/* ---------------------------------------------------------------------------------------- */
+/* Status of the bounded split-K waits                                                      */
+/* ---------------------------------------------------------------------------------------- */
+
+extern "C" int w4a16_split_wait_status(void *stream) {
+    hipStream_t s = (hipStream_t)stream;
+    unsigned count = 0;
+    int st = hip_status(hipMemcpyFromSymbolAsync(&count, HIP_SYMBOL(g_slot_wait_timeouts),
+                                                 sizeof(count), 0, hipMemcpyDeviceToHost, s),
+                        "split_wait_status read");
+    if (st) return st;
+    if ((st = hip_status(hipStreamSynchronize(s), "split_wait_status sync"))) return st;
+    if (count == 0) return W4A16_OK;
+    const unsigned zero = 0;
+    st = hip_status(hipMemcpyToSymbolAsync(HIP_SYMBOL(g_slot_wait_timeouts), &zero, sizeof(zero),
+                                           0, hipMemcpyHostToDevice, s),
+                    "split_wait_status clear");
+    if (!st) st = hip_status(hipStreamSynchronize(s), "split_wait_status sync");
+    if (st) return st;
+    return set_error(W4A16_ERR_HIP,
+                     "split_wait_status: %u split-K combine wait(s) gave up on an unwritten "
+                     "partial since the last check; outputs of the calls in between are wrong",
+                     count);
+}
+
+extern "C" int w4a16_debug_slot_wait(void *slot, int polls, float *out, void *stream) {
+    if (!slot || !out || polls < 0)
+        return set_error(W4A16_ERR_CONFIG, "debug_slot_wait: null pointer or negative bound");
+    if (misaligned(slot) || misaligned(out))
+        return set_error(W4A16_ERR_CONFIG, "debug_slot_wait: device buffers must be 16-byte aligned");
+    launch_k(slot_wait_probe_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream,
+                       reinterpret_cast<uint64_t *>(slot), polls, out);
+    return hip_status(hipGetLastError(), "debug_slot_wait launch");
+}
+
+extern "C" int w4a16_time_next_launch(int skip, void *start_event, void *stop_event) {
+    if (skip < 0) return set_error(W4A16_ERR_CONFIG, "time_next_launch: skip %d is negative", skip);
+    t_launches_to_skip = skip;
+    t_next_launch_events[0] = (hipEvent_t)start_event;
+    t_next_launch_events[1] = (hipEvent_t)stop_event;
+    return W4A16_OK;
 }

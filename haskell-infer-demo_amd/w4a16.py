@@ -64,6 +64,9 @@ _SIGNATURES = {
     "mlp_int4_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mlp_int4_bf16_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "w4a16_rmsnorm_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, ctypes.c_float, _vp]),
+    "w4a16_split_wait_status": (_i, [_vp]),
+    "w4a16_time_next_launch": (_i, [_i, _vp, _vp]),
+    "w4a16_debug_slot_wait": (_i, [_vp, _i, _vp, _vp]),
     "mlp_int4_norm_bf16": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i,
                                 _i, _vp]),
     "mlp_int4_norm_partial_f32": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -164,6 +167,12 @@ def _dev(t, nbytes, elem, what, device=None):
     if have < nbytes:
         raise W4A16Error(W4A16_ERR_CONFIG, f"{what}: {have} bytes, the call needs {nbytes}")
     return t.data_ptr()
+
+
+def split_wait_status(stream=None):
+    """Raise W4A16Error if a split-K combine wait gave up on the current device since the last
+    check (synchronises the stream; reads and clears the device's count)."""
+    _check(lib.w4a16_split_wait_status(_stream(stream)), "split_wait_status")
 
 
 def _check_ffn(h, inter, gu, dn, what):

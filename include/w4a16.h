@@ -327,6 +327,32 @@ int engine_ffn_forward_residual_norm(W4A16Store *store, int layer, uint16_t *res
                                      void *stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Status of the split-K combines (no counterpart in the reference, whose kernels have no
+ * cross-block waits).
+ *
+ * The split-K kernels finish a tile in the last of its blocks to arrive, which waits (bounded)
+ * for each partner's partial. A wait that gives up leaves a wrong output and counts itself in a
+ * per-device word. w4a16_split_wait_status synchronises `stream`, reads and clears the current
+ * device's word, and returns W4A16_OK, or W4A16_ERR_HIP with the count in w4a16_last_error()
+ * when any wait gave up since the previous check (a hip error of its own is also returned).
+ * ------------------------------------------------------------------------------------- */
+int w4a16_split_wait_status(void *stream);
+
+/* Test hook for the path above: one wave waits at most `polls` polls on the 8-byte slot at
+ * device address `slot` (16-byte aligned; a slot whose high half is zero is unwritten), stores
+ * what it took into out[0] (0.0 when the wait gave up) and clears the slot. The wait ends on
+ * its own, whatever the slot holds. Asynchronous on `stream`. */
+int w4a16_debug_slot_wait(void *slot, int polls, float *out, void *stream);
+
+/* Measurement hook (no counterpart in the reference): of the calling thread's next kernel
+ * launches by this library, the one after `skip` untimed launches records `start_event` /
+ * `stop_event` (hipEvent_t, either may be NULL) at that dispatch's own start and end, through
+ * hipExtLaunchKernel; later launches are untimed until the next call. bench.py uses it to time
+ * one kernel of a call live, on the stream it is launched on, as a kernel trace times it
+ * (skip = 1: the down kernel of an FFN call). W4A16_OK, or W4A16_ERR_CONFIG for skip < 0. */
+int w4a16_time_next_launch(int skip, void *start_event, void *stop_event);
+
+/* ---------------------------------------------------------------------------------------
  * Test bridges (host pointers, artifact layout; synchronous).
  * ------------------------------------------------------------------------------------- */
 
