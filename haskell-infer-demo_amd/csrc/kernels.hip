@@ -1334,12 +1334,24 @@ __global__ __launch_bounds__(1024) void gemv_rows16_kernel(
  * gate/up kernels inside the FFN entry points): the A operands of one MFMA are then 64 M
  * contiguous bytes, M / 2 whole cache lines, where the row-major rows give 16 half lines. The
  * A stream is what bounds this kernel (down at M = 16 without its A loads: 6.0 us against
- * 13.1), and the chunk-major order takes it from 13.1 to 8.6-8.7 us. */
+ * 13.1), and the chunk-major order takes it from 13.1 to 8.6-8.7 us.
+ *
+ * More than 16 row-major rows (gemm_int4_bf16 beyond M = 16): blockIdx.y takes rows
+ * 16 y .. 16 y + 15, so the slices run in one launch and their blocks read each weight tile at
+ * about the same time (the repeats are served by the caches). */
 template <bool OUT_F32, int NL, int D, bool CM>
 __global__ __launch_bounds__(1024) void gemv_rows16x_kernel(
     const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
     const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K,
     uint16_t *residual) {
+    if (!CM && blockIdx.y > 0) {
+        const int m0 = (int)blockIdx.y * 16;
+        x += (size_t)m0 * K;
+        out = static_cast<char *>(out) + (size_t)m0 * N * (OUT_F32 ? 4 : 2);
+        if (residual) residual += (size_t)m0 * N;
+        M -= m0;
+    }
+    if (M > 16) M = 16;
     constexpr int SK = 16;
     __shared__ f32x4_t red[SK * 64];
     const int G = K >> 7;
@@ -1866,8 +1878,8 @@ int launch_rows16x_nl(const uint16_t *x, int M, const uint8_t *w, const uint16_t
                       int N, int K, hipStream_t stream, uint16_t *residual) {
     constexpr int D = NL <= 5 ? NL : NL <= 9 ? 4 : 3;
     const int pairs = (N / 8 + 1) / 2;
-    launch_k((gemv_rows16x_kernel<OUT_F32, NL, D, CM>), dim3(pairs), dim3(1024), 0, stream,
-                       x, M, w, s, out, N, K, residual);
+    launch_k((gemv_rows16x_kernel<OUT_F32, NL, D, CM>), dim3(pairs, CM ? 1 : (M + 15) / 16),
+             dim3(1024), 0, stream, x, M, w, s, out, N, K, residual);
     return hip_status(hipGetLastError(), "gemv rows16x launch");
 }
 
@@ -2219,6 +2231,12 @@ static int run_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *
     constexpr bool F32 = OUT == kOutF32;
     const int out_cols = PAIR ? N / 2 : N;
     const size_t out_elem = F32 ? 4 : 2;
+    /* beyond 16 rows (no pair, row-major): all the 16-row slices in one launch of the
+     * registers-fed kernel, and at exactly 16 rows where the LDS-staged kernel cannot hold K */
+    if (!PAIR && !cm && (M > 16 || (M == 16 && rows16_smem(16, K, 16) > kMaxLds))) {
+        const int st = launch_rows16x<F32>(x, M, w, s, out, N, K, stream);
+        if (st <= 0) return st;
+    }
     for (int m0 = 0; m0 < M; m0 += 16) {
         const int rows = std::min(16, M - m0);
         const uint16_t *xs = x + (size_t)m0 * K;

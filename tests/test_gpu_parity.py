@@ -142,6 +142,22 @@ def test_small_m_parity(cuda, m):
     assert_parity(out, oracle.gemm_bf16(x, p, s, n, k), f"gemm M={m}")
 
 
+@pytest.mark.parametrize("m,n", [(16, 4096), (32, 4096), (40, 1024), (64, 1024), (100, 512),
+                                 (128, 1024)])
+def test_m_sweep_parity(cuda, m, n):
+    """The reference's --time sweep shape (K = 5120; reference tests/test_quantization_kernel.py:
+    162-216 times M = 1..128 at N = 4096): at 16 rows the registers-fed long-K kernel (the staged
+    rows would not fit LDS), past 16 all the 16-row slices in one launch of it, a ragged last
+    slice at 40 and 100 rows."""
+    k = 5120
+    say(f"gemm M={m} n={n} k={k}")
+    p, s = make_weight(n, k, seed=500 + m)
+    x = oracle.synth_activation(m, k, seed=600 + m)
+    w = w4a16.TiledWeight.from_artifact(p, s, n, k, device=cuda)
+    out = from_dev(w4a16.gemm_int4_bf16(to_dev(x, cuda), w))
+    assert_parity(out, oracle.gemm_bf16(x, p, s, n, k), f"gemm M={m} {n}x{k}")
+
+
 @pytest.mark.parametrize("m", [2, 3, 4, 5, 6, 7, 8, 9, 12, 15, 16])
 def test_few_rows_parity(cuda, m):
     """2 <= M <= 16 on the few-row MFMA kernels, through each of their block shapes: 1 group
