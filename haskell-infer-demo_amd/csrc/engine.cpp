@@ -260,9 +260,9 @@ extern "C" W4A16Store *w4a16_engine_create(const W4A16EngineConfig *cfg) {
         set_error(W4A16_ERR_CONFIG, "engine_create: bad configuration");
         return nullptr;
     }
-    if (c.int4_max_rows < 0 || c.int4_max_rows > c.max_tokens) {
-        set_error(W4A16_ERR_CONFIG, "engine_create: int4_max_rows %d is outside 0..max_tokens (%d)",
-                  c.int4_max_rows, c.max_tokens);
+    if (c.int4_max_rows < 0 || c.int4_max_rows > c.max_tokens || c.int4_max_rows > 16) {
+        set_error(W4A16_ERR_CONFIG, "engine_create: int4_max_rows %d is outside 0..min(16, "
+                  "max_tokens = %d)", c.int4_max_rows, c.max_tokens);
         return nullptr;
     }
     if (c.intermediate % c.tp_size != 0) {

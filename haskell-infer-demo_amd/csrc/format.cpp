@@ -40,6 +40,8 @@ extern "C" const char *w4a16_last_error(void) { return error_text(); }
 /* BF16 and the shape rule                                                                   */
 /* ---------------------------------------------------------------------------------------- */
 
+extern "C" int w4a16_abi_version(void) { return W4A16_ABI_VERSION; }
+
 extern "C" uint16_t w4a16_f32_to_bf16(float value) { return bf16_rne(value); }
 
 extern "C" float w4a16_bf16_to_f32(uint16_t bits) { return bf16_widen(bits); }

@@ -2102,6 +2102,15 @@ int fixed_scratch(hipStream_t stream, unsigned char **base) {
     if (dev < 0 || dev >= 64) return set_error(W4A16_ERR_CONFIG, "device ordinal %d out of range", dev);
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_fixed_base[dev]) {
+        /* the one-time clear below must run, not be recorded into a graph that may never be
+         * replayed: the first call on a device is refused under capture */
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        st = hip_status(hipStreamIsCapturing(stream, &cap), "hipStreamIsCapturing");
+        if (st) return st;
+        if (cap != hipStreamCaptureStatusNone)
+            return set_error(W4A16_ERR_STATE, "mlp_int4_bf16_noalloc: the first call on device %d "
+                             "clears the static scratch and must be made outside graph capture",
+                             dev);
         void *p = nullptr;
         st = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
         if (st) return st;

@@ -64,6 +64,7 @@ _SIGNATURES = {
     "mlp_int4_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mlp_int4_bf16_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "w4a16_rmsnorm_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, ctypes.c_float, _vp]),
+    "w4a16_abi_version": (_i, []),
     "w4a16_split_wait_status": (_i, [_vp]),
     "w4a16_time_next_launch": (_i, [_i, _vp, _vp]),
     "w4a16_debug_slot_wait": (_i, [_vp, _i, _vp, _vp]),

@@ -50,6 +50,13 @@ extern "C" {
 #define W4A16_GROUP 128
 #define W4A16_TILE_ROWS 8
 
+/* Version of this ABI (no reference counterpart). 2: W4A16EngineConfig gained its trailing
+ * int4_max_rows field and the store handle is W4A16Store (was EngineHandle); a caller built
+ * against version 1 passes a shorter config struct and must be rebuilt. w4a16_abi_version()
+ * returns the version the library was built with, so a binding can refuse a mismatch. */
+#define W4A16_ABI_VERSION 2
+int w4a16_abi_version(void);
+
 /* Thread-local reason for the last failure on this thread ("" if none).
  * Replaces linear_last_error / quant_manifest_last_error / engine_last_error
  * (reference csrc/linear_weight.cpp:16-28, csrc/quant_manifest.c:29-41). */

@@ -78,4 +78,10 @@ def assert_parity(got_bits, ref, what, rel_l2=1e-3, max_ulp=2.0, ref_is_bits=Tru
           f"(max own {m['max_ulp_own']:.3g})", flush=True)
     assert m["rel_l2"] <= rel_l2, (what, m)
     assert m["max_ulp"] <= max_ulp, (what, m)
+    # Elements past 2 ULPs of their own value (all near zero, admitted by the floor above):
+    # over the whole GPU suite 0.009% of the elements. A kernel-stage check may hold at most
+    # 0.1% of its elements (and a handful), an end-to-end check (floor rms/16) 1%, so the floor
+    # cannot hide a systematic error.
+    own_cap = m["n"] // (1000 if floor_div >= 64.0 else 100)
+    assert m["n_over_2ulp_own"] <= max(8, own_cap), (what, m)
     return m

@@ -118,13 +118,17 @@ def test_engine_keeps_its_own_loader(stub_engine):
 
 
 def test_int4_row_switch_refusals():
-    """The routing switch on the host: int4_max_rows outside 0..max_tokens is refused at create;
+    """The routing switch on the host: int4_max_rows outside 0..min(16, max_tokens) is refused at
+    create;
     a store routes one decode row by default (reference csrc/kernels/layers.cu:126) and refuses
     more rows before any device work; an unloaded layer is never routed."""
     with pytest.raises(w4a16.W4A16Error):
         w4a16.Engine(2, 256, 384, max_tokens=4, int4_max_rows=5)
     with pytest.raises(w4a16.W4A16Error):
         w4a16.Engine(2, 256, 384, max_tokens=4, int4_max_rows=-1)
+    with pytest.raises(w4a16.W4A16Error, match="min\\(16"):   # the small-M kernels stop at 16
+        w4a16.Engine(2, 256, 384, max_tokens=32, int4_max_rows=17)
+    w4a16.Engine(2, 256, 384, max_tokens=32, int4_max_rows=16).close()
     eng = w4a16.Engine(2, 256, 384, max_tokens=16)
     assert not eng.routes_int4(0, 1) and not eng.routes_int4(0, 4, verify_rows=True)
     for tokens in (2, 4, 16):
