@@ -223,6 +223,10 @@ int load_impl(W4A16Store *eng, const std::string &root) {
     if (!on_device.entered && (st = on_device.enter(eng->device))) return st;
     DevBuf ws;
     if (ws.alloc((size_t)eng->int4_rows * (size_t)(H + li) * 2)) return W4A16_ERR_WEIGHTS;
+    /* the split-K scratch at its worst case for this store's shapes, so forwards never allocate
+     * (or synchronise), also on the first call of a shape under graph capture */
+    if ((st = reserve_split_scratch(eng->int4_rows, (int)H, (int)li)))
+        return set_error(W4A16_ERR_WEIGHTS, "%s", join_error("split-K scratch: ").c_str());
     /* commit: only now does the handle see the new operands */
     eng->layers.swap(staged);
     eng->act_ws = std::move(ws);

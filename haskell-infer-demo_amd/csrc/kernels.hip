@@ -2323,6 +2323,23 @@ extern "C" int mlp_int4_bf16(const uint16_t *normed, const uint8_t *gup, const u
     return mlp_common(normed, gup, gus, dnp, dns, out, false, act_ws, M, hidden, inter, stream);
 }
 
+/* Grows the per-device split-K scratch (current device) to the worst case of every FFN call of
+ * 1..max_rows rows at this shape, so that such calls never allocate afterwards. The loader calls
+ * it once per store, outside any capture. */
+int reserve_split_scratch(int max_rows, int hidden, int inter) {
+    size_t pb = 0, nc = 0;
+    for (int m = 1; m <= std::max(1, std::min(max_rows, 16)); ++m) {
+        size_t a, b, c, d;
+        split_bound(m, 2 * inter, hidden, &a, &b);
+        split_bound(m, hidden, inter, &c, &d);
+        pb = std::max(pb, std::max(a, c));
+        nc = std::max(nc, std::max(b, d));
+    }
+    uint64_t *partial = nullptr;
+    unsigned *counters = nullptr;
+    return split_scratch(pb, nc, &partial, &counters);
+}
+
 extern "C" int mlp_int4_bf16_noalloc(const uint16_t *normed, const uint8_t *gup,
                                      const uint16_t *gus, const uint8_t *dnp, const uint16_t *dns,
                                      uint16_t *out, uint16_t *act_ws, int M, int hidden, int inter,

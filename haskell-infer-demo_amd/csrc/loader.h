@@ -100,4 +100,8 @@ int artifact_read(const std::string &root, const Artifact &a, const char *want_d
 
 }  // namespace w4a16
 
+/* Grows the current device's split-K scratch to the worst case of every FFN call of 1..max_rows
+ * rows at this hidden/intermediate (kernels.hip), so the store's forwards never allocate. */
+int reserve_split_scratch(int max_rows, int hidden, int inter);
+
 #endif /* W4A16_LOADER_H */

@@ -25,9 +25,10 @@
  *     sublayer may alias its output exactly).
  *   - Compute calls that overlap in time on one device must be ordered on one stream: the
  *     split-K kernels of the small-M path share one per-device scratch buffer. The first call
- *     of a shape may grow that buffer (an allocation and a device synchronisation), so make it
- *     before capturing calls into a HIP graph, or use mlp_int4_bf16_noalloc, which never
- *     allocates.
+ *     of a shape through the stateless entry points may grow that buffer (an allocation and a
+ *     device synchronisation), so make it before capturing calls into a HIP graph, or use
+ *     mlp_int4_bf16_noalloc, which never allocates. A store's loader reserves the buffer for
+ *     every shape its forwards can take, so engine_ffn_forward* never allocate.
  */
 #ifndef W4A16_H
 #define W4A16_H

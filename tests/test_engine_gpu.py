@@ -241,3 +241,46 @@ def test_engine_loads_converted_checkpoint(cuda, tmp_path):
         assert_parity(got.view(np.uint16), ref, f"converted layer {layer}", floor_div=16.0)
     assert not eng.routes_int4(1, 1)                    # the MoE layer keeps BF16
     eng.close()
+
+
+FIRST_FORWARD_CAPTURED = r"""
+import sys, tempfile
+sys.path[:0] = [sys.argv[1], sys.argv[1] + "/haskell-infer-demo_amd"]
+import numpy as np, torch, convert, w4a16
+from oracle import oracle
+H, I = 1024, 25600                       # 16 rows: the split-K MFMA down projection
+out_dir = tempfile.mkdtemp()
+convert.write_sidecar(out_dir, {0: {"mlpGate": oracle.synth_weight(I, H, 11),
+                                    "mlpUp": oracle.synth_weight(I, H, 12),
+                                    "mlpDown": oracle.synth_weight(H, I, 13)}}, "/tmp/synthetic")
+eng = w4a16.Engine(1, H, I, max_tokens=16, int4_max_rows=16)
+assert eng.load_quantized_ffn(out_dir) == 0, eng.last_error()
+x = torch.from_numpy(oracle.synth_activation(16, H, 21).view(np.int16)).cuda()
+got = torch.zeros((16, H), dtype=torch.int16, device="cuda")
+stream = torch.cuda.Stream()
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=stream):
+    eng.forward(0, x, out=got, stream=stream.cuda_stream)
+graph.replay()
+torch.cuda.synchronize()
+want = eng.forward(0, x)
+torch.cuda.synchronize()
+print("first-forward-captured", bool(torch.equal(got, want)))
+"""
+
+
+def test_engine_first_forward_under_capture(cuda):
+    """In a fresh process, a store's very first forward of its largest shape (16 verify rows on
+    the split-K MFMA down projection) is captured into a HIP graph: the loader reserved the
+    split-K scratch, so the forward neither allocates nor synchronises, and the replay equals an
+    eager forward."""
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("engine first forward under capture, child process", flush=True)
+    proc = subprocess.run([sys.executable, "-c", FIRST_FORWARD_CAPTURED, root],
+                          capture_output=True, text=True, timeout=110)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    assert "first-forward-captured True" in proc.stdout, proc.stdout + proc.stderr
