@@ -24,10 +24,11 @@ and ``config.pass_us_per_call`` gives the median, min and max over the passes.
 Prints ONE JSON line.
 * ``roofline`` is the dominant kernel's (the fused gate/up/SiLU GEMV, or the linear):
   algorithmic bytes per launch (packed nibbles + BF16 scales of its weight) over its average
-  duration, measured live: --steps eager calls, the kernel's dispatch in each timed by the
-  start/end events of w4a16_time_next_launch (hipExtLaunchKernel), which are the dispatch's own
-  times, the ones a kernel trace reports. ``rocprof_avg_us`` / ``frac_from_rocprof`` quote the
-  committed rocprofv3 kernel-trace average of the same workload (profiles/) beside it.
+  duration. ``frac`` uses the rocprofv3 kernel-trace average of the same workload's committed
+  profile (profiles/kernel_avg_<config>.json, over the dispatches of the live-timing sections),
+  ``frac_live`` the live measurement: --steps eager calls, the kernel's dispatch in each timed
+  by the start/end events of w4a16_time_next_launch (hipExtLaunchKernel), whose window also
+  holds the dispatch's setup (about 1 us more than the trace's duration).
 * ``floor_us`` / ``floor`` (FFN configs): a pure streaming read of the call's bytes in one
   launch, as two dependent launches, and an empty launch pair, on the same rotation
   (libw4a16_floor.so).
@@ -419,8 +420,9 @@ def main():
     tag = f"config{args.config}" + (f"_m{m}" if args.config == 3 or (args.config == 5 and m != 1)
                                     else "")
     # The committed rocprofv3 summaries of the same configuration (profiles/): the kernel the
-    # dominant launch runs and its kernel-trace average (which the live figure above must agree
-    # with), and its HBM bytes per launch from FETCH_SIZE / WRITE_SIZE scaled by a plain copy.
+    # dominant launch runs and its kernel-trace average (the figure `frac` uses; the live event
+    # window above runs about 1 us longer), and its HBM bytes per launch from FETCH_SIZE /
+    # WRITE_SIZE scaled by a plain copy.
     kdoc, rocprof_src = profile_json("kernel_avg", tag)
     dom_kernel = kdoc.get("dominant", {}).get("kernel")
     # the trace average over the dispatches of the live-timing sections (the context the live
@@ -434,6 +436,7 @@ def main():
     if not traffic:
         traffic_src = None
     dom_name = f"{dom_kernel or 'gemv'} ({dom_role})"
+    achieved_rp = dom_bytes / (rocprof_avg * 1e-6) / 1e9 if rocprof_avg else None
     ffn_gbs = per_set / (us_per_call * 1e-6) / 1e9
     srt = sorted(per_pass)
     pass_stats = {"passes": len(per_pass), "median": round(srt[len(srt) // 2], 3),
@@ -460,18 +463,24 @@ def main():
                                                "(w4a16_time_next_launch), eager launches"},
                    "with_rmsnorm_us_per_call": None if norm_us is None else round(norm_us, 3),
                    "with_residual_rmsnorm_us_per_call": None if f2_us is None else round(f2_us, 3)},
-        "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": dom_name,
+                     # achieved / frac from the kernel-trace average of this workload's committed
+                     # profile (its live-timing sections); the live event window beside it
+                     "achieved": round(achieved_rp if rocprof_avg else achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "traffic_source": traffic_src, "bytes_per_launch": dom_bytes,
-                     "avg_launch_us": round(k1_live, 3),
-                     "avg_launch_source": "live: dispatch start/end events of each launch, eager calls "
-                                          "enqueued back to back behind a spin kernel",
-                     "graph_us_per_launch": round(k1_graph, 3),
+                     "frac": round((achieved_rp if rocprof_avg else achieved) / HBM_PEAK_GBS, 4),
+                     "frac_source": "rocprof_avg_us" if rocprof_avg else "avg_launch_us_live",
+                     "traffic": traffic, "traffic_source": traffic_src,
+                     "bytes_per_launch": dom_bytes,
                      "rocprof_avg_us": rocprof_avg, "rocprof_avg_us_all_dispatches": rocprof_all,
                      "rocprof_source": rocprof_src,
-                     "frac_from_rocprof": None if not rocprof_avg else
-                     round(dom_bytes / (rocprof_avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+                     "avg_launch_us_live": round(k1_live, 3),
+                     "frac_live": round(achieved / HBM_PEAK_GBS, 4),
+                     "live_source": "dispatch start/end events of each launch "
+                                    "(w4a16_time_next_launch), eager calls enqueued back to back "
+                                    "behind a spin kernel; the event window also holds the "
+                                    "dispatch's setup",
+                     "graph_us_per_launch": round(k1_graph, 3)},
     }
     if not linear_only:
         floor = floor_us(torch, dev, count, dom_bytes, down_bytes, events, timed_fn=timed,
