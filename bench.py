@@ -15,9 +15,9 @@ reference publishes its per-call INT4 figures for (N=4096, K=5120: 52.1 us at M=
 reference docs/plan-numeric-contract.md:1753, and its --time sweep at M = 2 / 16 / 64 / 128,
 :1775-1778), at M = --m or over --m-sweep, quoted beside this run's.
 
-Timing: the calls of one pass over the rotating sets are captured in a HIP graph (and the first
-steps % sets calls in a second graph); exactly --steps calls are replayed in the timed region,
-with a HIP event on the replay stream before it and after every pass, so ``value`` is device
+Timing: the calls of one pass over the rotating sets are captured in a HIP graph (the first
+pass's graph also holds the steps % sets extra calls); exactly --steps calls are replayed in
+the timed region, with a HIP event on the replay stream before it and after every pass, so ``value`` is device
 time per call over all --steps calls (gaps between kernels included, not Python's launch rate)
 and ``config.pass_us_per_call`` gives the median, min and max over the passes.
 
@@ -288,9 +288,9 @@ def main():
 
     ffn_call, first_kernel = make_calls(x, act, out)
 
-    # Launches are captured into HIP graphs (one graph = one pass over all rotating weight sets,
-    # plus one holding the first steps % count calls) so the timed region measures the device,
-    # not Python's launch rate.
+    # Launches are captured into HIP graphs (one graph = one pass over all rotating weight sets;
+    # the first pass's graph also holds the steps % count extra calls) so the timed region
+    # measures the device, not Python's launch rate.
     def capture(fn, n=None):
         n = count if n is None else n
         for i in range(n):              # eager warm-up of exactly the captured work
@@ -307,14 +307,24 @@ def main():
         """Exactly `steps` calls of fn, replayed from graphs, after at least `warmup` untimed
         calls; returns (device us per call over all steps, wall us per call, per-pass us per
         call list)."""
-        full = capture(fn)
+        # one graph per pass over the rotating sets; the steps % count extra calls ride in the
+        # first pass's graph (a separate short graph would add a whole graph launch to few calls)
         rest = steps % count
-        tail = capture(fn, rest) if rest else None
+        if steps < count:
+            first = capture(fn, steps)
+            passes = [(first, steps)]
+            full = first
+        else:
+            full = capture(fn)
+            first = capture(fn, count + rest) if rest else full
+            passes = [(first, count + rest)] + [(full, count)] * (steps // count - 1)
         for _ in range(max(1, -(-warmup // count))):
+            full.replay()
+        if first is not full:   # its first replay uploads the graph: keep that out of the timing
+            first.replay()
             full.replay()
         torch.cuda.synchronize()
         stream = torch.cuda.current_stream()
-        passes = [(full, count)] * (steps // count) + ([(tail, rest)] if tail else [])
         evs = [torch.cuda.Event(enable_timing=True) for _ in range(len(passes) + 1)]
         t0 = time.perf_counter()
         evs[0].record(stream)
