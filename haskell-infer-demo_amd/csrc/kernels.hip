@@ -1459,6 +1459,131 @@ __global__ __launch_bounds__(1024) void gemv_rows16x_kernel(
     }
 }
 
+/* Beyond 16 row-major rows (gemm_int4_bf16): gemv_rows16x_kernel's layout (16 waves a block,
+ * wave ks taking groups ks + 16 i, A loaded per lane from memory, one LDS meeting at the end),
+ * but a wave takes TPW adjacent tile pairs and runs each A operand against all of them, so a
+ * block reads its 16 rows of A once for TPW tile pairs: the A bytes the CUs take in (every block
+ * reads all of K for its rows) shrink TPW times. blockIdx.y takes rows 16 y .. 16 y + 15. */
+template <bool OUT_F32, int NL, int D, int TPW>
+__global__ __launch_bounds__(1024) void gemv_rows16w_kernel(
+    const uint16_t *__restrict__ x, int M, const uint8_t *__restrict__ wt,
+    const uint16_t *__restrict__ st, void *__restrict__ out, int N, int K) {
+    {
+        const int m0 = (int)blockIdx.y * 16;
+        x += (size_t)m0 * K;
+        out = static_cast<char *>(out) + (size_t)m0 * N * (OUT_F32 ? 4 : 2);
+        M = min(16, M - m0);
+    }
+    constexpr int SK = 16;
+    extern __shared__ f32x4_t redw[]; /* [SK][TPW][64 lanes] */
+    const int G = K >> 7;
+    const int tiles = N >> 3;
+    const int lane = threadIdx.x & 63;
+    const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4;
+    const int n = lane & 15;
+    const int r = n & 7;
+    int tile[TPW];
+#pragma unroll
+    for (int p = 0; p < TPW; ++p) tile[p] = 2 * ((int)blockIdx.x * TPW + p) + (n >> 3);
+
+    /* 1. every scale, then every weight piece of this wave (a tile past N reads zeros) */
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wt, (uint32_t)((size_t)N * K / 2));
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(st, (uint32_t)((size_t)N * G * 2));
+    uint4 buf[NL][TPW];
+    uint16_t sbits[NL][TPW];
+#pragma unroll
+    for (int i = 0; i < NL; ++i)
+#pragma unroll
+        for (int p = 0; p < TPW; ++p) {
+            const int g = ks + i * SK;
+            const bool ok = tile[p] < tiles && g < G;
+            const uint32_t unit = (uint32_t)(tile[p] * G + g);
+            sbits[i][p] = buf_load_u16(sr, ok ? unit * 16 + (uint32_t)r * 2 : kOob);
+        }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+#pragma unroll
+        for (int p = 0; p < TPW; ++p) {
+            const int g = ks + i * SK;
+            const bool ok = tile[p] < tiles && g < G;
+            const uint32_t unit = (uint32_t)(tile[p] * G + g);
+            buf[i][p] = buf_load16_stream(wr, ok ? unit * 512 + (uint32_t)(q * 8 + r) * 16 : kOob);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    /* 2. the A operands of group i: for MFMA t, row n, k = 128 g + 32 t + 8 q .. + 7 */
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)M * K * 2);
+    const bool row_ok = n < M;
+    const uint32_t row_off = (uint32_t)(n * K + q * 8) * 2;
+    uint4 av[D][4];
+    auto load_a = [&](int i) {
+        const int g = ks + i * SK;
+        const bool ok = row_ok && g < G;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            av[i % D][t] = buf_load16(xr, ok ? row_off + (uint32_t)(g * 128 + 32 * t) * 2 : kOob);
+    };
+#pragma unroll
+    for (int i = 0; i < D && i < NL; ++i) load_a(i);
+
+    /* 3. per group and tile pair, four product MFMAs and four offset MFMAs, as rows16x */
+    const uint4 offs = make_uint4(0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u, 0xBF40BF40u);
+    f32x4_t acc[TPW];
+#pragma unroll
+    for (int p = 0; p < TPW; ++p) acc[p] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        if (ks + i * SK < G) { /* wave-uniform */
+#pragma unroll
+            for (int p = 0; p < TPW; ++p) {
+                const uint32_t words[4] = {buf[i][p].x, buf[i][p].y, buf[i][p].z, buf[i][p].w};
+                f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const bf16x8_t a = __builtin_bit_cast(bf16x8_t, av[i % D][t]);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, unpack8(words[t]), d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, offs),
+                                                                d, 0, 0, 0);
+                }
+                const float sc = bf16_widen(sbits[i][p]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[p][j] = fmaf(sc, d[j], acc[p][j]);
+            }
+        } else {
+#pragma unroll
+            for (int p = 0; p < TPW; ++p) asm volatile("" ::"v"(buf[i][p].x), "v"(sbits[i][p]));
+        }
+        if (i + D < NL) load_a(i + D);
+    }
+
+    /* 4. the 16 waves in LDS, summed in wave order; lane (n, q) holds rows 4 q + j of column n */
+#pragma unroll
+    for (int p = 0; p < TPW; ++p) redw[(ks * TPW + p) * 64 + lane] = acc[p];
+    __syncthreads();
+    if (ks >= TPW) return;
+    const int p = ks; /* wave p finishes tile pair p */
+    f32x4_t sum = redw[p * 64 + lane];
+    for (int w = 1; w < SK; ++w) {
+        const f32x4_t v = redw[(w * TPW + p) * 64 + lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sum[j] += v[j];
+    }
+    const int tl = 2 * ((int)blockIdx.x * TPW + p) + (n >> 3);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m = 4 * q + j;
+        if (m < M && tl < tiles) {
+            const size_t o = (size_t)m * N + tl * 8 + r;
+            const float row_sum = 32.0f * sum[j];
+            if (OUT_F32) reinterpret_cast<float *>(out)[o] = row_sum;
+            else reinterpret_cast<uint16_t *>(out)[o] = bf16_rne(row_sum);
+        }
+    }
+}
+
 /* RMSNorm of each row (one block a row): BF16(x * rsqrt(sum x^2 / cols + eps) * (bias + w)),
  * FP32 arithmetic (reference csrc/kernels/flashinfer_norm.cu:22-76). Each thread holds CH
  * 8-value chunks of the row, all loaded before any use, so a row costs one load round trip;
@@ -1899,6 +2024,38 @@ int launch_rows16x(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s
     return 1;
 }
 
+/* Beyond 16 row-major rows: gemv_rows16w_kernel with as many tile pairs a wave (4, 2 or 1) as
+ * still leaves a block a CU across the 16-row slices. Returns 1 when K is beyond its shapes. */
+template <bool OUT_F32, int NL, int TPW>
+int launch_rows16w_t(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
+                     int N, int K, hipStream_t stream) {
+    constexpr int D = TPW >= 4 ? 1 : 2;
+    const int pairs = (N / 8 + 1) / 2;
+    launch_k((gemv_rows16w_kernel<OUT_F32, NL, D, TPW>), dim3((pairs + TPW - 1) / TPW, (M + 15) / 16),
+             dim3(1024), (size_t)16 * TPW * 64 * sizeof(f32x4_t), stream, x, M, w, s, out, N, K);
+    return hip_status(hipGetLastError(), "gemv rows16w launch");
+}
+
+template <bool OUT_F32, int NL>
+int launch_rows16w_nl(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out,
+                      int N, int K, hipStream_t stream) {
+    const int pairs = (N / 8 + 1) / 2;
+    const int slices = (M + 15) / 16;
+    const int cus = device_cus();
+    if ((pairs / 4) * slices >= cus) return launch_rows16w_t<OUT_F32, NL, 4>(x, M, w, s, out, N, K, stream);
+    if ((pairs / 2) * slices >= cus) return launch_rows16w_t<OUT_F32, NL, 2>(x, M, w, s, out, N, K, stream);
+    return 1;
+}
+
+template <bool OUT_F32>
+int launch_rows16w(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
+                   int K, hipStream_t stream) {
+    const int nl = (K / 128 + 15) / 16;
+    if (nl <= 2) return launch_rows16w_nl<OUT_F32, 2>(x, M, w, s, out, N, K, stream);
+    if (nl <= 3) return launch_rows16w_nl<OUT_F32, 3>(x, M, w, s, out, N, K, stream);
+    return 1;
+}
+
 template <bool PAIR, bool OUT_F32>
 int launch_rows16(const uint16_t *x, int M, const uint8_t *w, const uint16_t *s, void *out, int N,
                   int K, hipStream_t stream, int cm = 0) {
@@ -2242,6 +2399,10 @@ static int run_rows(const uint16_t *x, int M, const uint8_t *w, const uint16_t *
     const size_t out_elem = F32 ? 4 : 2;
     /* beyond 16 rows (no pair, row-major): all the 16-row slices in one launch of the
      * registers-fed kernel, and at exactly 16 rows where the LDS-staged kernel cannot hold K */
+    if (!PAIR && !cm && M > 16) {
+        const int st = launch_rows16w<F32>(x, M, w, s, out, N, K, stream);
+        if (st <= 0) return st;
+    }
     if (!PAIR && !cm && (M > 16 || (M == 16 && rows16_smem(16, K, 16) > kMaxLds))) {
         const int st = launch_rows16x<F32>(x, M, w, s, out, N, K, stream);
         if (st <= 0) return st;

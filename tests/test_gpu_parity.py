@@ -142,12 +142,14 @@ def test_small_m_parity(cuda, m):
     assert_parity(out, oracle.gemm_bf16(x, p, s, n, k), f"gemm M={m}")
 
 
-@pytest.mark.parametrize("m,n", [(16, 4096), (32, 4096), (40, 1024), (64, 1024), (100, 512),
-                                 (128, 1024)])
+@pytest.mark.parametrize("m,n", [(16, 4096), (32, 4096), (40, 1024), (64, 1024), (64, 4096),
+                                 (100, 512), (100, 4096), (128, 1024)])
 def test_m_sweep_parity(cuda, m, n):
     """The reference's --time sweep shape (K = 5120; reference tests/test_quantization_kernel.py:
     162-216 times M = 1..128 at N = 4096): at 16 rows the registers-fed long-K kernel (the staged
-    rows would not fit LDS), past 16 all the 16-row slices in one launch of it, a ragged last
+    rows would not fit LDS), past 16 all the 16-row slices in one launch, on the kernel that runs
+    each A operand against two tile pairs (32 rows at N = 4096, 128 rows at N = 1024) or four
+    (64 and 100 rows at N = 4096) where that still leaves a block a CU, else one; a ragged last
     slice at 40 and 100 rows."""
     k = 5120
     say(f"gemm M={m} n={n} k={k}")
